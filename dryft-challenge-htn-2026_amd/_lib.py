@@ -1,0 +1,77 @@
+"""ctypes binding of libdryft_decode.so (the C ABI declared in include/dryft_decode.h).
+
+torch is imported before the library is opened: torch ships its own libamdhip64 with the same
+soname as the system one, so loading torch first makes the library bind to torch's HIP runtime
+and torch's stream handles and device pointers are valid in every call.
+
+There is no fallback: if the library is missing or fails to load, ``lib()`` raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (load order: see module docstring)
+
+LIB_NAME = "libdryft_decode.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_Z = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "dd_abi_version": (_I, []),
+    "dd_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
+    "dd_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
+    "dd_gemv": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "dd_gemv_splitk": (_I, [_I, _I, _I]),
+    "dd_gemv_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "dd_gemv_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P]),
+    "dd_gate_up_silu": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "dd_silu_mul": (_I, [_P, _P, _I, _I, _P]),
+    "dd_qkv_post_decode": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _P,
+                                _I, _I, _I, _I, _I, _I, _F, _P, _P]),
+    "dd_attn_decode": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "dd_attn_chunk": (_I, [_I, _I, _I]),
+    "dd_attn_ws_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),
+    "dd_embed_rmsnorm": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P, _P]),
+    "dd_argmax": (_I, [_P, _I, _I, _P, _P, _I, _P]),
+    "dd_stream_read": (_I, [_P, _Z, _I, _I, _P, _P]),
+}
+
+_LIB = None
+
+
+def exported_symbols():
+    """Names of every C-ABI entry point this binding declares."""
+    return sorted(_SIGS)
+
+
+def lib():
+    """Load (once) and return the library with argument types declared."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_NAME} is not built ({LIB_PATH}); run `python -c 'import __graft_entry__ as g; "
+            "g.build()'` from the repository root")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    v = handle.dd_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"{LIB_NAME} ABI version {v}, binding expects {ABI_VERSION}")
+    _LIB = handle
+    return _LIB
+
+
+def check(status, name):
+    """Raise on a nonzero status from a C-ABI call."""
+    if status != 0:
+        what = "invalid argument" if status == 1 else f"hipError {status}"
+        raise RuntimeError(f"{name} failed: {what}")

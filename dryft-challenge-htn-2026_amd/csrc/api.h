@@ -1,0 +1,31 @@
+// Host-side helpers shared by the C-ABI entry points (see include/dryft_decode.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/dryft_decode.h"
+
+#define DD_API extern "C" __attribute__((visibility("default")))
+
+namespace dd {
+
+constexpr int DD_ABI_VERSION = 1;
+
+inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+
+// Launch result: the error of the last launch on this thread (0 when it went through).
+inline int launch_status() { return (int)hipGetLastError(); }
+
+// GEMV launch helpers (gemv.hip): split-K choice, k per split, and the partial-sum launch
+// (returns the number of splits launched; with partials, or when > 1 split, fp32 partials land
+// in ws[split][M][N], otherwise bf16 y).
+int pick_splitk(int M, int N, int K);
+int kps_for(int K, int sk);
+int launch_gemv(const void* x, const void* W, void* y, void* ws, int M, int N, int K, int sk,
+                bool partials, hipStream_t stream);
+
+}  // namespace dd
+
+#define DD_REQUIRE(cond)                         \
+  do {                                           \
+    if (!(cond)) return (int)hipErrorInvalidValue; \
+  } while (0)

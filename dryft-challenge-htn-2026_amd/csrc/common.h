@@ -1,0 +1,83 @@
+// Shared device helpers for the gfx950 decode-step kernels.
+//
+// Conventions
+//  * bf16 tensors are passed as raw 16-bit patterns (uint16_t); arithmetic is fp32.
+//  * fp32 -> bf16 conversion is round-to-nearest-even (the rounding torch and the reference's
+//    kernels use at every bf16 cast point).
+//  * wave64 everywhere; MFMA tiles are v_mfma_f32_16x16x32_bf16 with the gfx950 operand layout
+//      A (16x32): lane l holds A[l%16][(l/16)*8 + i], i = 0..7
+//      B (32x16): lane l holds B[(l/16)*8 + i][l%16]
+//      D (16x16): lane l holds D[(l/16)*4 + i][l%16], i = 0..3
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dd {
+
+typedef uint16_t bf16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+
+__device__ __forceinline__ float bf2f(bf16 v) { return __uint_as_float(((unsigned)v) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quietened).
+__device__ __forceinline__ bf16 f2bf(float f) {
+  unsigned u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16)(u >> 16);
+}
+
+// Round an fp32 value to the nearest bf16 value, returned as fp32.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// low / high bf16 of a packed 32-bit word
+__device__ __forceinline__ float lo_bf(unsigned w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 16-byte global load; the pointer must be 16-byte aligned.
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+// 16-byte global load that streams past the caches (weights are read once per step).
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+// Wave-wide reductions (64 lanes). xor-shuffles give every lane the full result.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Sum over a workgroup of NW waves; deterministic order (wave partials added in wave order).
+// `red` must hold at least NW floats of shared memory. Every thread gets the result.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// 1/sqrt with IEEE sqrt and IEEE divide (torch.rsqrt on the CPU is 1/sqrt in fp32).
+__device__ __forceinline__ float rsqrt_ieee(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+}  // namespace dd

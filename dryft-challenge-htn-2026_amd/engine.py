@@ -1,0 +1,378 @@
+"""Qwen3-shape greedy-decode engine on MI355X: static KV cache, hipGraph-captured decode step,
+pipelined host loop, decode kernels from libdryft_decode.so.
+
+Mirrors the reference ``Engine`` API (engine/engine.py:247-279, 683-732):
+``Engine(model_path)`` loads an HF-named safetensors checkpoint, ``generate(input_ids, n)``
+yields one ``list[int]`` (one token per sequence) per step. Plain greedy decoding only (the
+reference's speculative and fp8 paths are not part of this build).
+
+Differences by design (MI355X-first):
+  * decode positions are per row (``st.pos`` is ``[B]``), so a ragged batch decodes in ONE state
+    and one weight pass per step instead of the reference's per-length groups
+    (engine.py:1093-1105); each row's tokens are the ones the reference produces for that
+    sequence on its own;
+  * one state (and one captured graph) serves every prompt length of a (B, cap) shape;
+  * ``ops`` is :class:`HipOps`; a failed load-time self-test raises instead of falling back to
+    torch (``ENGINE_OPS=torch`` selects the torch ops explicitly, for diagnostics).
+"""
+import glob
+import json
+import math
+import os
+
+import torch
+
+from .hipops import HipOps, TorchOps
+
+CAP_GRAN = 128        # engine.py:24
+MAX_STATES = 6        # engine.py:94
+ROPE_LEN = 32768      # engine.py:96
+
+
+def rope_theta(cfg):
+    """RoPE base from an HF config: top-level ``rope_theta`` (transformers 4.x, what
+    engine.py:258 reads) or ``rope_parameters.rope_theta`` (transformers 5.x)."""
+    if "rope_theta" in cfg:
+        return float(cfg["rope_theta"])
+    return float(cfg["rope_parameters"]["rope_theta"])
+
+
+def build_rope_tables(theta, hd, n, dtype=torch.bfloat16):
+    """engine.py:118-122, evaluated with torch on the CPU (then uploaded) so the tables are the
+    same bits on every machine: inv = 1/theta^(2j/hd) fp32; emb = cat(f, f); cos/sin -> dtype."""
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2).float() / hd))
+    fr = torch.outer(torch.arange(n).float(), inv)
+    emb = torch.cat((fr, fr), -1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+class _Layer:
+    pass
+
+
+class _State:
+    pass
+
+
+class _Mixed:
+    """Diagnostics: HIP ops with some groups swapped for torch ops (ENGINE_OFF=attn,qkv,gemv);
+    the reference's _Mixed contract (engine.py:221-236)."""
+
+    GROUPS = {
+        "attn": ("attn_decode",),
+        "attnp": ("attn_prefill",),
+        "qkv": ("qkv_post",),
+        "gemv": ("linear", "gate_up_silu", "linear_add_norm"),
+    }
+
+    def __init__(self, fused, ref, off):
+        self.f, self.r = fused, ref
+        self.off = {name for g in off for name in self.GROUPS.get(g, ())}
+
+    def __getattr__(self, name):
+        return getattr(self.r if name in self.off else self.f, name)
+
+
+class Engine:
+    def __init__(self, model_path=None, dtype=torch.bfloat16, device=None, selftest=True,
+                 _cfg=None, _weights=None):
+        self.dev = torch.device(device) if device is not None else torch.device("cuda")
+        if self.dev.type != "cuda":
+            raise RuntimeError("the HIP decode engine needs a GPU (device 'cuda')")
+        self.dtype = dtype
+        if _cfg is None:
+            with open(os.path.join(model_path, "config.json")) as f:
+                _cfg = json.load(f)
+        cfg = _cfg
+        self.cfg = cfg
+        self.L = cfg["num_hidden_layers"]
+        self.nh = cfg["num_attention_heads"]
+        self.nkv = cfg["num_key_value_heads"]
+        self.hd = cfg.get("head_dim") or cfg["hidden_size"] // self.nh
+        self.eps = cfg["rms_norm_eps"]
+        self.theta = rope_theta(cfg)
+        if _weights is None:
+            from safetensors.torch import load_file
+            _weights = {}
+            for fn in sorted(glob.glob(os.path.join(model_path, "*.safetensors"))):
+                _weights.update(load_file(fn, device=str(self.dev)))
+        self._load(dict(_weights))
+        self._build_rope(ROPE_LEN)
+        self.states = {}
+        self._dbg = None
+        self.pool = torch.cuda.graph_pool_handle()
+        self.ops = self._select_ops(selftest)
+
+    @classmethod
+    def from_state_dict(cls, cfg, weights, **kw):
+        return cls(None, _cfg=cfg, _weights=weights, **kw)
+
+    # ---------------------------------------------------------------- weights
+    def _load(self, w):
+        """engine.py:282-308: fused wqkv = cat(q, k, v), wgu = cat(gate, up), tied lm_head."""
+        g = lambda k: w.pop(k).to(device=self.dev, dtype=self.dtype)
+        self.embed = g("model.embed_tokens.weight").contiguous()
+        self.lm_head = g("lm_head.weight").contiguous() if "lm_head.weight" in w else self.embed
+        self.norm = g("model.norm.weight")
+        self.layers = []
+        for i in range(self.L):
+            p = f"model.layers.{i}."
+            l = _Layer()
+            l.ln1 = g(p + "input_layernorm.weight")
+            l.ln2 = g(p + "post_attention_layernorm.weight")
+            l.qn = g(p + "self_attn.q_norm.weight")
+            l.kn = g(p + "self_attn.k_norm.weight")
+            l.wqkv = torch.cat([g(p + f"self_attn.{n}_proj.weight") for n in "qkv"], 0).contiguous()
+            l.wo = g(p + "self_attn.o_proj.weight").contiguous()
+            l.wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")],
+                              0).contiguous()
+            l.wd = g(p + "mlp.down_proj.weight").contiguous()
+            self.layers.append(l)
+
+    def _build_rope(self, n):
+        cos, sin = build_rope_tables(self.theta, self.hd, n, self.dtype)
+        self.cos, self.sin = cos.to(self.dev), sin.to(self.dev)
+
+    def _grow_rope(self, cap):
+        """engine.py:322-331: rebuild the tables; graphs baked the old addresses, so drop them
+        and start a fresh graph pool."""
+        self.states.clear()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        self.pool = torch.cuda.graph_pool_handle()
+        self._build_rope(cap)
+
+    # ---------------------------------------------------------------- ops selection
+    def _select_ops(self, selftest):
+        if os.environ.get("ENGINE_OPS") == "torch":
+            return TorchOps(self)
+        ops = None
+        errors = []
+        candidates = (("full", True), ("without GEMV", False)) if selftest else (("full", True),)
+        for label, use_gemv in candidates:
+            cand = HipOps(self, use_gemv=use_gemv)
+            if not selftest:
+                ops = cand
+                break
+            try:
+                diff = self._selftest(cand)
+                print(f"[engine] HIP ops {label} selftest max logit diff {diff:.4f}")
+                if diff <= 0.5:
+                    ops = cand
+                    break
+                errors.append(f"{label}: diff {diff:.4f}")
+            except Exception as ex:  # report and try the next rung
+                errors.append(f"{label}: {ex!r}")
+        if ops is None:
+            raise RuntimeError("HIP decode ops failed their self-test: " + "; ".join(errors))
+        off = [x for x in os.environ.get("ENGINE_OFF", "").split(",") if x]
+        if off:
+            ops = _Mixed(ops, TorchOps(self), off)
+        return ops
+
+    def _selftest(self, candidate):
+        """engine.py:629-680 contract: prefill B=2, S=96, then 3 teacher-forced decode steps with
+        the candidate ops vs torch ops on the same weights; returns the max logit difference."""
+        torch.manual_seed(0)
+        B, S, n = 2, 96, 4
+        high = min(5000, self.embed.shape[0])
+        ids = torch.randint(min(100, high - 1), high, (B, S), device=self.dev)
+
+        def run(ops, forced=None):
+            saved = self.ops
+            self.ops = ops
+            try:
+                st = self._new_state(B, 128)
+                self._dbg, toks = [], []
+                self._prefill(ids.tolist(), st)
+                for t in range(n):
+                    toks.append(st.tok.clone())
+                    if t < n - 1:
+                        if forced is not None:
+                            st.tok.copy_(forced[t])
+                        self._decode_body(st)
+                return self._dbg, toks
+            finally:
+                self._dbg = None
+                self.ops = saved
+
+        ref, toks = run(TorchOps(self))
+        got, _ = run(candidate, toks)
+        diffs = [(r - g).abs().max().item() for r, g in zip(ref, got)]
+        return max(diffs) if all(math.isfinite(d) for d in diffs) else float("inf")
+
+    # ---------------------------------------------------------------- state
+    def _new_state(self, B, cap, W=1):
+        """engine.py:343-356 (zeros KV [B, nkv, cap, hd] per layer) with per-row positions."""
+        st = _State()
+        st.B, st.cap, st.W = B, cap, W
+        shape = (B, self.nkv, cap, self.hd)
+        # zeros, not empty: masked slots must be finite (0 * NaN = NaN)
+        st.kc = [torch.zeros(shape, dtype=self.dtype, device=self.dev) for _ in range(self.L)]
+        st.vc = [torch.zeros(shape, dtype=self.dtype, device=self.dev) for _ in range(self.L)]
+        st.tok = torch.zeros(B * W, dtype=torch.long, device=self.dev)
+        st.pos = torch.zeros(B, dtype=torch.long, device=self.dev)
+        st.graph = None
+        st.hcap = 0
+        return st
+
+    def _state(self, B, cap, W=1, graph=True):
+        key = (B, cap, W, graph)
+        st = self.states.get(key)
+        if st is not None:
+            return st
+        if len(self.states) >= MAX_STATES:
+            del self.states[next(iter(self.states))]
+            torch.cuda.empty_cache()
+        st = self._new_state(B, cap, W)
+        self.states[key] = st
+        if graph:
+            try:
+                self._capture(st)
+            except Exception as e:  # fall back to eager decode (engine.py:365-370)
+                print(f"[engine] graph capture failed for {key}: {e!r}")
+                st.graph = None
+        return st
+
+    def _capture(self, st):
+        """engine.py:380-396: warm up on a side stream, then capture one decode step. Positions
+        are reset afterwards (the warm-ups and the capture advance them)."""
+        st.pos.zero_()
+        dbg, self._dbg = self._dbg, None       # no host copies inside the captured step
+        try:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    self._decode_body(st)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self.pool):
+                self._decode_body(st)
+            st.graph = g
+            torch.cuda.synchronize()
+        finally:
+            self._dbg = dbg
+        st.pos.zero_()
+        st.tok.zero_()
+
+    def _host_bufs(self, st, n):
+        if st.hcap < n:
+            st.hcap = max(n, 256)
+            st.host = torch.empty((st.hcap, st.B), dtype=torch.long, pin_memory=True)
+            st.events = [torch.cuda.Event() for _ in range(st.hcap)]
+
+    # ---------------------------------------------------------------- forward
+    def _forward(self, st, tokens, S, pos):
+        """engine.py:459-503 layer loop. pos=None: prefill from position 0 (logits of each
+        sequence's last token); pos=[B] tensor: decode of S tokens per row starting at pos[b].
+        Returns bf16 logits."""
+        B = st.B
+        ops = self.ops
+        decode = pos is not None
+        if decode and hasattr(ops, "embed_rms"):
+            h, a = ops.embed_rms(tokens, self.embed, self.layers[0].ln1)
+        else:
+            h = self.embed[tokens]
+            a = ops.rms(h, self.layers[0].ln1)
+        last = self.L - 1
+        for i, l in enumerate(self.layers):
+            kc, vc = st.kc[i], st.vc[i]
+            qkv = ops.linear(a, l.wqkv)
+            q = ops.qkv_post(qkv, l, kc, vc, B, S, pos, last_query_only=not decode and i == last)
+            if decode:
+                o = ops.attn_decode(q, kc, vc, pos, S)
+            elif i == last:
+                o = ops.attn_prefill(q, kc, vc, S, last_query_only=True)
+                h = h[S - 1::S].contiguous()
+            else:
+                o = ops.attn_prefill(q, kc, vc, S)
+            h, a = ops.linear_add_norm(o, l.wo, h, l.ln2)
+            m = ops.gate_up_silu(a, l.wgu)
+            h, a = ops.linear_add_norm(m, l.wd, h, self.layers[i + 1].ln1 if i < last else self.norm)
+        logits = ops.linear(a, self.lm_head)
+        if self._dbg is not None:
+            self._dbg.append(logits.float().cpu())
+        return logits
+
+    def _decode_body(self, st):
+        """engine.py:538-540: tok <- argmax(forward(tok, pos)); pos += 1 (fused in one kernel)."""
+        logits = self._forward(st, st.tok, st.W, st.pos)
+        if hasattr(self.ops, "argmax_"):
+            self.ops.argmax_(logits, st.tok, st.pos)
+        else:
+            st.tok.copy_(logits.argmax(-1))
+            st.pos.add_(1)
+
+    def _prefill(self, input_ids, st):
+        """Prompt pass (engine.py:505-515, eager). Equal lengths: one batched pass. Ragged: one
+        pass per sequence into its own cache row. Sets st.tok and st.pos[b] = len(prompt b)."""
+        lens = [len(x) for x in input_ids]
+        if len(set(lens)) == 1:
+            ids = torch.tensor(input_ids, dtype=torch.long, device=self.dev)
+            B, S = ids.shape
+            st.tok.copy_(self._forward(st, ids.reshape(-1), S, None).argmax(-1))
+        else:
+            dbg = self._dbg
+            rows = []
+            for b, seq in enumerate(input_ids):
+                sub = _State()
+                sub.B = 1
+                sub.kc = [k[b:b + 1] for k in st.kc]
+                sub.vc = [v[b:b + 1] for v in st.vc]
+                ids = torch.tensor([seq], dtype=torch.long, device=self.dev)
+                self._dbg = [] if dbg is not None else None
+                st.tok[b:b + 1].copy_(self._forward(sub, ids.reshape(-1), len(seq), None).argmax(-1))
+                if dbg is not None:
+                    rows.append(self._dbg[-1])
+            self._dbg = dbg
+            if dbg is not None:
+                dbg.append(torch.cat(rows, 0))
+        st.pos.copy_(torch.tensor(lens, dtype=torch.long, device=self.dev))
+
+    # ---------------------------------------------------------------- generate
+    @torch.inference_mode()
+    def generate(self, input_ids, max_new_tokens):
+        """engine.py:683-732 plain path: prefill, then n-1 graph replays; the host copies step t's
+        tokens into pinned memory and yields step t-1 while step t runs."""
+        if max_new_tokens <= 0:
+            return
+        n = max_new_tokens
+        B = len(input_ids)
+        S = max(len(x) for x in input_ids)
+        cap = -(-(S + n) // CAP_GRAN) * CAP_GRAN
+        if cap > self.cos.shape[0]:
+            self._grow_rope(cap)
+        st = self._state(B, cap, graph=n > 1)
+        self._host_bufs(st, n)
+        self._prefill(input_ids, st)
+        host, ev = st.host, st.events
+        host[0].copy_(st.tok, non_blocking=True)
+        ev[0].record()
+        for t in range(1, n):
+            if st.graph is not None:
+                st.graph.replay()
+            else:
+                self._decode_body(st)
+            host[t].copy_(st.tok, non_blocking=True)
+            ev[t].record()
+            ev[t - 1].synchronize()
+            yield host[t - 1].tolist()
+        ev[n - 1].synchronize()
+        yield host[n - 1].tolist()
+
+    # ---------------------------------------------------------------- verify shape
+    @torch.inference_mode()
+    def verify_logits(self, st, tokens, spos):
+        """Multi-query (verify-shaped) forward: row (b, s) is token tokens[b, s] at position
+        spos[b] + s, causal within the W rows (engine.py:542-547; fused.py:438-441, 492-503).
+        Writes K/V at spos[b] + s and returns logits [B*W, V]."""
+        B, W = tokens.shape
+        return self._forward(st, tokens.reshape(-1).contiguous(), W, spos)
+
+    def error_flags(self):
+        """Device error word of the kernels (1: token id out of range, 2: position outside the
+        cache / rope table). Synchronises."""
+        ops = self.ops.f if isinstance(self.ops, _Mixed) else self.ops
+        return int(ops.err.item()) if hasattr(ops, "err") else 0

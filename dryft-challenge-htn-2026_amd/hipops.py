@@ -1,0 +1,296 @@
+"""``HipOps``: the engine's ops object backed by the gfx950 HIP kernels of libdryft_decode.so.
+
+Drop-in for the reference's ``TritonOps`` (engine/fused.py:880-1059): same constructor
+``HipOps(e, use_gemv=True)``, same methods, same argument meaning, same output layouts, and the
+same fallback contract for inputs the kernels do not take (``F.linear`` for non-bf16,
+non-contiguous or M > BM_MAX inputs; torch for the prefill branch of ``qkv_post`` and for
+``attn_prefill``, which are outside the decode step). ``e`` carries ``dev, eps, nh, nkv, hd,
+cos, sin`` like the reference's engine (test_fused.py:20-22).
+
+Every decode-step method calls the C ABI on torch's current stream; outputs and workspaces are
+allocated with ``torch.empty`` (so they come from the graph pool under capture). A nonzero
+status raises ``RuntimeError``.
+"""
+import torch
+import torch.nn.functional as F
+
+from ._lib import check, lib
+
+BM_MAX = 16  # largest activation-row count the skinny GEMV takes (fused.py:838 BM_MAX role)
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _bf16_ok(*ts):
+    return all(t.dtype == torch.bfloat16 and t.is_contiguous() and t.is_cuda for t in ts)
+
+
+# -- torch helpers for the prefill branch (outside the decode step; same arithmetic as the
+#    reference's _rms / _rope, engine.py:107-115) -----------------------------------------------
+def _rms_t(x, w, eps):
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(x.dtype)
+
+
+def _rope_t(x, cos, sin):
+    h = x.shape[-1] // 2
+    return x * cos + torch.cat((-x[..., h:], x[..., :h]), -1) * sin
+
+
+def _qkv_post_prefill_t(e, qkv, l, kc, vc, B, S, last_query_only):
+    """Prefill branch of qkv_post (engine.py:172-181) in torch on the GPU: positions 0..S-1."""
+    nh, nkv, hd = e.nh, e.nkv, e.hd
+    q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], -1)
+    q = q.reshape(B, S, nh, hd)
+    if last_query_only:
+        q = q[:, -1:, :, :]
+    q = _rms_t(q, l.qn, e.eps).transpose(1, 2)
+    k = _rms_t(k.reshape(B, S, nkv, hd), l.kn, e.eps).transpose(1, 2)
+    v = v.reshape(B, S, nkv, hd).transpose(1, 2)
+    cos, sin = e.cos[:S], e.sin[:S]
+    qcos, qsin = (cos[-1:], sin[-1:]) if last_query_only else (cos, sin)
+    q, k = _rope_t(q, qcos, qsin), _rope_t(k, cos, sin)
+    kc[:, :, :S] = k
+    vc[:, :, :S] = v
+    return q
+
+
+class HipOps:
+    """Ops object of the decode path on MI355X (gfx950)."""
+
+    def __init__(self, e, use_gemv=True):
+        self.e = e
+        self.use_gemv = use_gemv
+        assert e.hd & (e.hd - 1) == 0 and e.hd >= 2
+        self.L = lib()  # raises when the library is missing: no silent fallback
+        self._counters = None
+        self.err = torch.zeros(1, dtype=torch.int32, device=e.dev)
+
+    # ---------------------------------------------------------------- helpers
+    def _attn_counters(self, n, dev):
+        c = self._counters
+        if c is None or c.numel() < n or c.device != dev:
+            self._counters = torch.zeros(max(n, 256), dtype=torch.int32, device=dev)
+        return self._counters
+
+    def _gemv_ok(self, x, w):
+        M, K = x.shape
+        return (self.use_gemv and 1 <= M <= BM_MAX and _bf16_ok(x, w) and K % 8 == 0
+                and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+    # ---------------------------------------------------------------- norms
+    def rms(self, h, w):
+        h = h.contiguous()
+        if not _bf16_ok(h, w):
+            return _rms_t(h, w, self.e.eps)
+        M, N = h.reshape(-1, h.shape[-1]).shape
+        y = torch.empty_like(h)
+        check(self.L.dd_rmsnorm(_ptr(h), _ptr(w), _ptr(y), M, N, self.e.eps, _stream(h.device)),
+              "dd_rmsnorm")
+        return y
+
+    def add_rms(self, h, d, w):
+        h, d = h.contiguous(), d.contiguous()
+        if not _bf16_ok(h, d, w):
+            hn = h + d
+            return hn, _rms_t(hn, w, self.e.eps)
+        M, N = h.reshape(-1, h.shape[-1]).shape
+        hn = torch.empty_like(h)
+        y = torch.empty_like(h)
+        check(self.L.dd_add_rmsnorm(_ptr(h), _ptr(d), _ptr(w), _ptr(hn), _ptr(y), M, N,
+                                    self.e.eps, _stream(h.device)), "dd_add_rmsnorm")
+        return hn, y
+
+    def silu_mul(self, gu):
+        gu = gu.contiguous()
+        M, I2 = gu.shape
+        out = torch.empty((M, I2 // 2), dtype=gu.dtype, device=gu.device)
+        if not _bf16_ok(gu):
+            g, u = gu.chunk(2, -1)
+            return F.silu(g) * u
+        check(self.L.dd_silu_mul(_ptr(gu), _ptr(out), M, I2 // 2, _stream(gu.device)),
+              "dd_silu_mul")
+        return out
+
+    # ---------------------------------------------------------------- GEMV family
+    def linear(self, x, w):
+        if not self._gemv_ok(x, w):
+            return F.linear(x, w)
+        M, K = x.shape
+        N = w.shape[0]
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+        sk = self.L.dd_gemv_splitk(M, N, K)
+        ws = None
+        if sk > 1:
+            ws = torch.empty(self.L.dd_gemv_ws_bytes(M, N, K, sk) // 4, dtype=torch.float32,
+                             device=x.device)
+        check(self.L.dd_gemv(_ptr(x), _ptr(w), _ptr(out), M, N, K, sk, _ptr(ws),
+                             _stream(x.device)), "dd_gemv")
+        return out
+
+    def gate_up_silu(self, x, wgu):
+        if not self._gemv_ok(x, wgu):
+            return self.silu_mul(self.linear(x, wgu))
+        M, K = x.shape
+        I = wgu.shape[0] // 2
+        out = torch.empty((M, I), dtype=x.dtype, device=x.device)
+        check(self.L.dd_gate_up_silu(_ptr(x), _ptr(wgu), _ptr(out), M, I, K, _stream(x.device)),
+              "dd_gate_up_silu")
+        return out
+
+    def linear_add_norm(self, x, w, h, lnw):
+        """hn = h + x @ w^T ; returns (hn, rmsnorm(hn, lnw))"""
+        if not (self._gemv_ok(x, w) and _bf16_ok(h, lnw)):
+            return self.add_rms(h, self.linear(x, w), lnw)
+        M, K = x.shape
+        N = w.shape[0]
+        sk = self.L.dd_gemv_splitk(M, N, K)
+        ws = torch.empty(self.L.dd_gemv_ws_bytes(M, N, K, sk) // 4, dtype=torch.float32,
+                         device=x.device)
+        hn = torch.empty_like(h)
+        y = torch.empty_like(h)
+        check(self.L.dd_gemv_add_rmsnorm(_ptr(x), _ptr(w), _ptr(h), _ptr(lnw), _ptr(hn), _ptr(y),
+                                         M, N, K, self.e.eps, sk, _ptr(ws), _stream(x.device)),
+              "dd_gemv_add_rmsnorm")
+        return hn, y
+
+    # ---------------------------------------------------------------- attention block
+    def qkv_post(self, qkv, l, kc, vc, B, S, pos, last_query_only=False):
+        e = self.e
+        if pos is None:
+            return self._qkv_post_prefill(qkv, l, kc, vc, B, S, last_query_only)
+        qkv = qkv.contiguous()
+        q = torch.empty((B, e.nh, S, e.hd), dtype=qkv.dtype, device=qkv.device)
+        pos_stride = 1 if pos.numel() > 1 else 0
+        check(self.L.dd_qkv_post_decode(
+            _ptr(qkv), _ptr(l.qn), _ptr(l.kn), _ptr(e.cos), _ptr(e.sin), e.cos.shape[0],
+            _ptr(pos), pos_stride, _ptr(q), _ptr(kc), _ptr(vc), B, S, e.nh, e.nkv, e.hd,
+            kc.shape[2], e.eps, _ptr(self.err), _stream(qkv.device)), "dd_qkv_post_decode")
+        return q
+
+    def attn_decode(self, q, kc, vc, pos, W=1):
+        """q: [B, nkv, W, G, hd] (from qkv_post). Token j of seq b attends to
+        kc/vc[b, :, :pos[b]+j+1]. -> [B*W, nh*hd]"""
+        e = self.e
+        B = q.shape[0]
+        cap = kc.shape[2]
+        chunk = self.L.dd_attn_chunk(B, e.nkv, cap)
+        out = torch.empty((B * W, e.nh * e.hd), dtype=q.dtype, device=q.device)
+        ws = torch.empty(max(1, self.L.dd_attn_ws_bytes(B, W, e.nh, e.nkv, e.hd, cap, chunk) // 4),
+                         dtype=torch.float32, device=q.device)
+        counters = self._attn_counters(B * e.nkv, q.device)
+        pos_stride = 1 if pos.numel() > 1 else 0
+        check(self.L.dd_attn_decode(_ptr(q.contiguous()), _ptr(kc), _ptr(vc), _ptr(pos), pos_stride,
+                                    _ptr(out), _ptr(ws), _ptr(counters), B, W, e.nh, e.nkv, e.hd,
+                                    cap, chunk, _stream(q.device)), "dd_attn_decode")
+        return out
+
+    # ---------------------------------------------------------------- prefill (torch)
+    def _qkv_post_prefill(self, qkv, l, kc, vc, B, S, last_query_only):
+        return _qkv_post_prefill_t(self.e, qkv, l, kc, vc, B, S, last_query_only)
+
+    def attn_prefill(self, q, kc, vc, S, last_query_only=False):
+        """Prefill attention (engine.py:148-152): torch SDPA on the GPU."""
+        e = self.e
+        return F.scaled_dot_product_attention(
+            q, kc[:, :, :S], vc[:, :, :S], is_causal=not last_query_only, enable_gqa=True
+        ).transpose(1, 2).reshape(-1, e.nh * e.hd)
+
+    # ---------------------------------------------------------------- step tail
+    def argmax_(self, logits, tok, pos=None):
+        """tok[:] = logits.argmax(-1); pos += 1 when given (engine.py:503, 539-540)."""
+        M, V = logits.shape
+        check(self.L.dd_argmax(_ptr(logits.contiguous()), M, V, _ptr(tok), _ptr(pos),
+                               0 if pos is None else pos.numel(), _stream(logits.device)),
+              "dd_argmax")
+        return tok
+
+    def embed_rms(self, tokens, embed, w):
+        """h = embed[tokens]; a = rms(h, w) (engine.py:467-468). -> (h, a)"""
+        M = tokens.numel()
+        V, N = embed.shape
+        h = torch.empty((M, N), dtype=embed.dtype, device=embed.device)
+        a = torch.empty_like(h)
+        check(self.L.dd_embed_rmsnorm(_ptr(tokens), _ptr(embed), V, _ptr(w), _ptr(h), _ptr(a), M,
+                                      N, self.e.eps, _ptr(self.err), _stream(embed.device)),
+              "dd_embed_rmsnorm")
+        return h, a
+
+
+class TorchOps:
+    """The reference's torch arithmetic (``_TorchOps``, engine.py:125-187) on the GPU, extended
+    to per-row positions ``pos[B]`` and verify widths W > 1. It is not the decode path: the
+    engine uses it for its load-time self-test and when ``ENGINE_OPS=torch`` asks for it."""
+
+    def __init__(self, e):
+        self.e = e
+
+    def linear(self, x, w):
+        return F.linear(x, w)
+
+    def rms(self, h, w):
+        return _rms_t(h, w, self.e.eps)
+
+    def add_rms(self, h, d, w):
+        hn = h + d
+        return hn, _rms_t(hn, w, self.e.eps)
+
+    def gate_up_silu(self, x, wgu):
+        return self.silu_mul(F.linear(x, wgu))
+
+    def linear_add_norm(self, x, w, h, lnw):
+        h = h + F.linear(x, w)
+        return h, _rms_t(h, lnw, self.e.eps)
+
+    def silu_mul(self, gu):
+        g, u = gu.chunk(2, -1)
+        return F.silu(g) * u
+
+    def attn_prefill(self, q, kc, vc, S, last_query_only=False):
+        e = self.e
+        return F.scaled_dot_product_attention(
+            q, kc[:, :, :S], vc[:, :, :S], is_causal=not last_query_only, enable_gqa=True
+        ).transpose(1, 2).reshape(-1, e.nh * e.hd)
+
+    def _positions(self, pos, B, S):
+        p = pos.reshape(-1)
+        p = p.expand(B) if p.numel() == 1 else p
+        return p[:, None] + torch.arange(S, device=p.device)[None, :]      # [B, S]
+
+    def attn_decode(self, q, kc, vc, pos, W=1):
+        e = self.e
+        B, cap = q.shape[0], kc.shape[2]
+        G = e.nh // e.nkv
+        P = self._positions(pos, B, W)                                      # [B, W]
+        lim = P.repeat_interleave(G, dim=1)                                 # row r = s*G + g
+        mask = torch.zeros((B, 1, W * G, cap), dtype=q.dtype, device=q.device)
+        mask.masked_fill_(torch.arange(cap, device=q.device)[None, None, None, :]
+                          > lim[:, None, :, None], float("-inf"))
+        o = F.scaled_dot_product_attention(q.reshape(B, e.nkv, W * G, e.hd), kc, vc,
+                                           attn_mask=mask)
+        return o.reshape(B, e.nkv, W, G, e.hd).permute(0, 2, 1, 3, 4).reshape(B * W, e.nh * e.hd)
+
+    def qkv_post(self, qkv, l, kc, vc, B, S, pos, last_query_only=False):
+        e = self.e
+        nh, nkv, hd = e.nh, e.nkv, e.hd
+        if pos is None:
+            return _qkv_post_prefill_t(e, qkv, l, kc, vc, B, S, last_query_only)
+        q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], -1)
+        P = self._positions(pos, B, S)                                      # [B, S]
+        cos, sin = e.cos[P][:, :, None, :], e.sin[P][:, :, None, :]         # [B, S, 1, hd]
+        q = _rope_t(_rms_t(q.reshape(B, S, nh, hd), l.qn, e.eps), cos, sin)
+        k = _rope_t(_rms_t(k.reshape(B, S, nkv, hd), l.kn, e.eps), cos, sin)
+        v = v.reshape(B, S, nkv, hd)
+        bi = torch.arange(B, device=qkv.device)[:, None].expand(B, S)
+        kc[bi, :, P] = k
+        vc[bi, :, P] = v
+        G = nh // nkv
+        qo = q.reshape(B, S, nkv, G, hd).permute(0, 2, 1, 3, 4).contiguous()  # [B, nkv, S, G, hd]
+        return qo.view(B, nh, S, hd)

@@ -1,0 +1,120 @@
+/* dryft_decode.h -- C ABI of the MI355X (gfx950) decode-step kernels.
+ *
+ * Drop-in boundary for the decode hot path of KrishP147/Dryft-Challenge-HTN-2026: each entry
+ * point replaces one method of the reference's ops object (``TritonOps`` in engine/fused.py,
+ * whose reference arithmetic is ``_TorchOps`` in engine/engine.py) or one step of
+ * ``Engine._forward`` / ``_decode_body``. The Python host (hipops.py) binds these with ctypes
+ * exactly where the reference launches its Triton kernels.
+ *
+ * Conventions
+ *  - All tensors are device pointers to contiguous row-major memory on the current HIP device.
+ *    bf16 tensors are passed as ``const void*`` / ``void*`` (16-bit patterns); fp32 workspaces
+ *    as ``void*``; positions and token ids as int64 (torch.long).
+ *  - Every call is asynchronous on ``stream`` and capture-safe: no allocation, no host sync,
+ *    positions are read from device memory.
+ *  - Return value: 0 on success; hipErrorInvalidValue (1) when an argument fails validation
+ *    (nothing is launched then); otherwise the hipError_t reported by the launch. Nothing throws
+ *    across the ABI.
+ *  - ``err`` (optional, may be NULL) is a device int that kernels OR flags into instead of
+ *    faulting: 1 = token id out of range (row 0 used), 2 = position outside cache/rope table
+ *    (row skipped).
+ */
+#ifndef DRYFT_DECODE_H
+#define DRYFT_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version (bumped on any signature change). */
+int dd_abi_version(void);
+
+/* y[m] = rmsnorm(x[m]) * w, m < M, row length N (N <= 4096).
+ * Replaces TritonOps.rms (fused.py:894-895; kernel fused.py:152-172), reference
+ * _TorchOps.rms / _rms (engine.py:107-110, 134-135). */
+int dd_rmsnorm(const void* x, const void* w, void* y, int M, int N, float eps, hipStream_t stream);
+
+/* hn = bf16(x + d); y = rmsnorm(hn) * w.
+ * Replaces TritonOps.add_rms (fused.py:897-898; kernel fused.py:152-172 with HAS_ADD). */
+int dd_add_rmsnorm(const void* x, const void* d, const void* w, void* hn, void* y, int M, int N,
+                   float eps, hipStream_t stream);
+
+/* y[M,N] = x[M,K] . W[N,K]^T (bf16 out, fp32 accumulate), 1 <= M <= 16, K % 8 == 0,
+ * x and W 16-byte aligned. splitk <= 0 picks the library's choice (dd_gemv_splitk); when the
+ * split is > 1, ws must hold split * M * N floats (dd_gemv_ws_bytes).
+ * Replaces TritonOps.linear (fused.py:989-1014; kernels fused.py:568-628), reference
+ * _TorchOps.linear = F.linear (engine.py:131-132). */
+int dd_gemv(const void* x, const void* W, void* y, int M, int N, int K, int splitk, void* ws,
+            hipStream_t stream);
+
+/* The split-K factor dd_gemv / dd_gemv_add_rmsnorm use for this shape when splitk <= 0.
+ * Replaces the shape-keyed tile table GEMM_CFG (fused.py:711-718, 773-789). */
+int dd_gemv_splitk(int M, int N, int K);
+size_t dd_gemv_ws_bytes(int M, int N, int K, int splitk);
+
+/* hn = bf16(h + bf16(x . W^T)); y = rmsnorm(hn) * lnw (N <= 4096).
+ * Replaces TritonOps.linear_add_norm (fused.py:1034-1059; kernels fused.py:568-618, 685-709),
+ * reference _TorchOps.linear_add_norm (engine.py:140-142). ws as for dd_gemv (always used). */
+int dd_gemv_add_rmsnorm(const void* x, const void* W, const void* h, const void* lnw, void* hn,
+                        void* y, int M, int N, int K, float eps, int splitk, void* ws,
+                        hipStream_t stream);
+
+/* out[M,I] = bf16(bf16(silu(g)) * u), [g | u] = x . Wgu^T, Wgu = [gate; up] of shape [2I, K].
+ * Replaces TritonOps.gate_up_silu (fused.py:1016-1032; kernel fused.py:631-682), reference
+ * _TorchOps.gate_up_silu (engine.py:137-138, 144-146). */
+int dd_gate_up_silu(const void* x, const void* Wgu, void* out, int M, int I, int K,
+                    hipStream_t stream);
+
+/* out[M,I] = bf16(bf16(silu(g)) * u) with gu[M, 2I] = [g | u].
+ * Replaces TritonOps.silu_mul (fused.py:900-906; kernel fused.py:175-188). */
+int dd_silu_mul(const void* gu, void* out, int M, int I, hipStream_t stream);
+
+/* Decode qkv_post: per-head q/k RMSNorm (qn/kn), RoPE at position pos[b*pos_stride] + s,
+ * k and v written to kc/vc[b, h, position], q written as [B, NKV, S, G, HD].
+ * qkv: [B*S, (NH + 2*NKV) * HD]; cos/sin: [rope_rows, HD] bf16 tables; HD must be 128.
+ * Replaces TritonOps.qkv_post with pos given (fused.py:932-941; kernel fused.py:415-475),
+ * reference _TorchOps.qkv_post decode branch (engine.py:166-187). */
+int dd_qkv_post_decode(const void* qkv, const void* qn, const void* kn, const void* cos_t,
+                       const void* sin_t, int rope_rows, const int64_t* pos, int pos_stride,
+                       void* q, void* kc, void* vc, int B, int S, int NH, int NKV, int HD, int cap,
+                       float eps, int* err, hipStream_t stream);
+
+/* Split-KV GQA decode attention with log-sum-exp combine.
+ * q: [B, NKV, W, G, HD] (dd_qkv_post_decode layout); kc/vc: [B, NKV, cap, HD] (zero-initialised);
+ * query row (b, s) sees keys 0 .. pos[b*pos_stride] + s. out: [B*W, NH*HD].
+ * chunk: keys per split (multiple of 32; <= 0 picks dd_attn_chunk). ws: dd_attn_ws_bytes bytes;
+ * counters: B*NKV ints, zero before the first call (kernels leave them zero).
+ * HD must be 128 and W*G <= 32.
+ * Replaces TritonOps.attn_decode (fused.py:961-987; kernels fused.py:478-565), reference
+ * _TorchOps.attn_decode (engine.py:154-164). */
+int dd_attn_decode(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                   int pos_stride, void* out, void* ws, int* counters, int B, int W, int NH,
+                   int NKV, int HD, int cap, int chunk, hipStream_t stream);
+int dd_attn_chunk(int B, int NKV, int cap);
+size_t dd_attn_ws_bytes(int B, int W, int NH, int NKV, int HD, int cap, int chunk);
+
+/* h[m] = embed[tok[m]]; y = rmsnorm(h) * w. embed: [V, N].
+ * Replaces the embedding gather + first ops.rms of Engine._forward (engine.py:467-468). */
+int dd_embed_rmsnorm(const int64_t* tok, const void* embed, int V, const void* w, void* h,
+                     void* y, int M, int N, float eps, int* err, hipStream_t stream);
+
+/* tok[m] = argmax(logits[m]) (first index on ties, NaN largest); then pos[i] += 1 for
+ * i < npos when pos is not NULL.
+ * Replaces logits.argmax(-1) and st.pos.add_(1) (engine.py:503, 538-540). */
+int dd_argmax(const void* logits, int M, int V, int64_t* tok, int64_t* pos, int npos,
+              hipStream_t stream);
+
+/* Measurement helper, no counterpart in the reference: streams `bytes` from p (16-byte words,
+ * nontemporal loads) with the given launch shape; used to measure the achievable HBM read
+ * bandwidth that decode-step throughput is reported against. */
+int dd_stream_read(const void* p, size_t bytes, int grid, int block, unsigned* sink,
+                   hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DRYFT_DECODE_H */

@@ -1,0 +1,32 @@
+"""CPU oracle for the decode-step hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU with plain PyTorch (and pure-Python bf16 helpers for tiny
+known-answer cases), the arithmetic of the reference engine's torch path
+(``engine/engine.py`` of KrishP147/Dryft-Challenge-HTN-2026). It is the checker that the HIP
+decode path is compared against.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it, and only as the checker / the timed CPU baseline -- never as the thing measured on the GPU
+and never as a fallback of the product path.
+
+Modules
+-------
+``reference``  ops (``TorchOps``) and a model/engine restatement (``OracleEngine``).
+``bf16``       round-to-nearest-even bf16 helpers in pure Python (known-answer tests).
+
+How each function is pinned (what makes a plausible mistake fail a test):
+
+* ``rms`` / ``add_rms`` / ``linear_add_norm``: closed-form known answers with hand-rounded bf16
+  (tests/test_oracle_known_answers.py, restating probe_gpu_no_torch.py:103-153, 627-688) and the
+  HF Qwen3 end-to-end test.
+* ``silu_mul`` / ``gate_up_silu``: closed form (probe_gpu_no_torch.py:73-98, 576-621).
+* ``qkv_post``: rotation special cases (identity, quarter turn, (0.75, 0.25)), V bit-exact, cache
+  tail untouched (probe_gpu_no_torch.py:158-328).
+* ``attn_decode``: structured closed form across a 64-key tile boundary
+  (probe_gpu_no_torch.py:333-401) and an independent fp64 loop (test_attn.py:14-24).
+* ``linear``: exact-sum structured inputs (probe_gpu_no_torch.py:467-572) and fp64 brute force.
+* ``build_rope_tables``: float64 closed form within one bf16 ulp, plus the HF rotary embedding.
+* ``OracleEngine`` (forward/generate/ragged/verify): token-exact against HF
+  ``Qwen3ForCausalLM.generate`` on the tiny fp32 config of test_vs_hf.py:13-35, and verify ==
+  sequential decode (engine.py:549-627).
+"""

@@ -1,0 +1,79 @@
+"""The C-ABI library loads, exports every entry point include/dryft_decode.h declares, and
+rejects bad arguments before launching anything (these calls never touch a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import dryft_amd
+from dryft_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "dryft_decode.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(dd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert header_symbols() == _lib.exported_symbols()
+
+
+def test_library_exports_every_symbol():
+    L = dryft_amd.lib()
+    for name in header_symbols():
+        assert hasattr(L, name), name
+    assert L.dd_abi_version() == _lib.ABI_VERSION
+
+
+def test_validation_rejects_without_launch():
+    L = dryft_amd.lib()
+    INVALID = 1
+    # null pointers
+    assert L.dd_gemv(None, None, None, 1, 16, 64, 1, None, None) == INVALID
+    assert L.dd_rmsnorm(None, None, None, 1, 16, 1e-6, None) == INVALID
+    # shape limits checked before any pointer is used (fake, never-dereferenced addresses)
+    fake = ctypes.c_void_p(0x1000)
+    assert L.dd_gemv(fake, fake, fake, 17, 16, 64, 1, None, None) == INVALID   # M > 16
+    assert L.dd_gemv(fake, fake, fake, 1, 16, 60, 1, None, None) == INVALID    # K % 8
+    assert L.dd_gemv(ctypes.c_void_p(0x1008), fake, fake, 1, 16, 64, 1, None, None) == INVALID
+    assert L.dd_rmsnorm(fake, fake, fake, 1, 5000, 1e-6, None) == INVALID    # N > 4096
+    assert L.dd_qkv_post_decode(fake, fake, fake, fake, fake, 64, fake, 0, fake, fake, fake,
+                                1, 1, 32, 8, 64, 128, 1e-6, None, None) == INVALID   # HD != 128
+    assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
+                            1, 9, 32, 8, 128, 128, 128, None) == INVALID         # W*G > 32
+    assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
+                            1, 1, 32, 8, 128, 128, 100, None) == INVALID         # chunk % 32
+
+
+def test_host_side_sizing():
+    L = dryft_amd.lib()
+    # split-K: keep >= 512 k per split, grow the grid toward 512 workgroups
+    for N, K in ((151936, 2560), (6144, 2560), (2560, 4096), (2560, 9728), (19456, 2560)):
+        sk = L.dd_gemv_splitk(16, N, K)
+        tiles = -(-N // 16)
+        assert sk >= 1 and K // sk >= 512
+        # stops once the grid reaches 512 workgroups or another split would go under 512 k
+        assert tiles * sk >= 512 or K // (2 * sk) < 512 or sk == 8
+    assert L.dd_gemv_splitk(16, 151936, 2560) == 1
+    for M, N, K in ((16, 2560, 4096), (1, 6144, 2560), (3, 64, 64)):
+        sk = L.dd_gemv_splitk(M, N, K)
+        assert L.dd_gemv_ws_bytes(M, N, K, sk) >= max(sk, 1) * M * N * 4
+    # attention: chunk multiple of 128, workspace covers every split of every row
+    for B, cap in ((1, 640), (16, 3072), (16, 8192)):
+        c = L.dd_attn_chunk(B, 8, cap)
+        assert c % 128 == 0 and c >= 128
+        nsplit = -(-cap // c)
+        assert L.dd_attn_ws_bytes(B, 1, 32, 8, 128, cap, c) == B * 8 * nsplit * 4 * 130 * 4
+
+
+@pytest.mark.parametrize("status", [0, 1, 700])
+def test_check_raises_on_nonzero(status):
+    if status == 0:
+        _lib.check(0, "x")
+    else:
+        with pytest.raises(RuntimeError):
+            _lib.check(status, "x")
