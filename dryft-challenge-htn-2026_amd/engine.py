@@ -101,6 +101,7 @@ class Engine:
         self.states = {}
         self._dbg = None
         self.pool = torch.cuda.graph_pool_handle()
+        self.ops = None
         self.ops = self._select_ops(selftest)
 
     @classmethod

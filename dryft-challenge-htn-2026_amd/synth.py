@@ -67,7 +67,7 @@ def tensor_shapes(cfg):
     return out
 
 
-@torch.inference_mode()
+@torch.no_grad()
 def random_weights(cfg, seed=0, device="cpu", dtype=torch.bfloat16, std=0.02):
     """dict name -> tensor, generated in ``tensor_shapes`` order from one seeded generator."""
     g = torch.Generator(device=device).manual_seed(seed)
