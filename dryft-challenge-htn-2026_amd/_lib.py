@@ -13,7 +13,7 @@ import torch  # noqa: F401  (load order: see module docstring)
 
 LIB_NAME = "libdryft_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -25,10 +25,12 @@ _SIGS = {
     "dd_abi_version": (_I, []),
     "dd_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "dd_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
-    "dd_gemv": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "dd_gemv": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
+    "dd_gemv_counters": (_I, [_I]),
     "dd_gemv_splitk": (_I, [_I, _I, _I]),
     "dd_gemv_ws_bytes": (_Z, [_I, _I, _I, _I]),
-    "dd_gemv_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P]),
+    "dd_gemv_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P]),
+    "dd_gemv_add_rmsnorm_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "dd_gate_up_silu": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "dd_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "dd_qkv_post_decode": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _P,
@@ -37,7 +39,8 @@ _SIGS = {
     "dd_attn_chunk": (_I, [_I, _I, _I]),
     "dd_attn_ws_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),
     "dd_embed_rmsnorm": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P, _P]),
-    "dd_argmax": (_I, [_P, _I, _I, _P, _P, _I, _P]),
+    "dd_argmax": (_I, [_P, _I, _I, _P, _P, _I, _P, _P, _P]),
+    "dd_argmax_ws_bytes": (_Z, [_I, _I]),
     "dd_stream_read": (_I, [_P, _Z, _I, _I, _P, _P]),
 }
 

@@ -190,8 +190,8 @@ attn_decode_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc,
   }
 
   // ---- merge the 4 waves, one 16-row block at a time ----
-  if (threadIdx.x == 0) sh.last = 0;
   const size_t wsrow = HD + 2;
+  const rsrc_t wsr = make_rsrc(ws, (unsigned)((size_t)gridDim.x * nsplit_max * R * wsrow * 4));
   for (int rb = 0; rb < RB; ++rb) {
     __syncthreads();  // V staging area is reused for the merge
 #pragma unroll
@@ -222,44 +222,35 @@ attn_decode_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc,
         const int sq = row / G, gq = row % G;
         out[((size_t)b * W + sq) * (NKV * G * HD) + ((size_t)kvh * G + gq) * HD + d] = f2bf(o / l);
       } else {
-        float* p = ws + (((size_t)bk * nsplit_max + split) * R + row) * wsrow;
-        p[d] = o;
+        const unsigned p = (unsigned)((((size_t)bk * nsplit_max + split) * R + row) * wsrow) * 4;
+        stc_f32(wsr, p + d * 4, o);
         if (d == 0) {
-          p[HD] = M;
-          p[HD + 1] = l;
+          stc_f32(wsr, p + HD * 4, M);
+          stc_f32(wsr, p + (HD + 1) * 4, l);
         }
       }
     }
   }
   if (nsplit == 1) return;
 
-  // ---- last split to arrive combines (split order) ----
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = atomicAdd(&counters[bk], 1);
-    sh.last = (old == nsplit - 1);
-  }
-  __syncthreads();
-  if (!sh.last) return;
-  __threadfence();
+  // ---- last split to arrive combines (split order); partials travel through sc1 ----
+  if (!arrive_last(counters + bk, nsplit, &sh.last)) return;
   for (int e = threadIdx.x; e < R * HD; e += ATT_THREADS) {
     const int row = e / HD, d = e % HD;
-    const float* p = ws + ((size_t)bk * nsplit_max * R + row) * wsrow;
-    const size_t sstride = (size_t)R * wsrow;
+    const unsigned p = (unsigned)(((size_t)bk * nsplit_max * R + row) * wsrow) * 4;
+    const unsigned sstride = (unsigned)(R * wsrow) * 4;
     float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, __builtin_nontemporal_load(p + sp * sstride + HD));
+    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, ldc_f32(wsr, p + sp * sstride + HD * 4));
     float o = 0.f, l = 0.f;
     for (int sp = 0; sp < nsplit; ++sp) {
-      const float* ps = p + sp * sstride;
-      const float f = exp2f(__builtin_nontemporal_load(ps + HD) - M);
-      o += __builtin_nontemporal_load(ps + d) * f;
-      l += __builtin_nontemporal_load(ps + HD + 1) * f;
+      const unsigned ps = p + sp * sstride;
+      const float f = exp2f(ldc_f32(wsr, ps + HD * 4) - M);
+      o += ldc_f32(wsr, ps + d * 4) * f;
+      l += ldc_f32(wsr, ps + (HD + 1) * 4) * f;
     }
     const int sq = row / G, gq = row % G;
     out[((size_t)b * W + sq) * (NKV * G * HD) + ((size_t)kvh * G + gq) * HD + d] = f2bf(o / l);
   }
-  if (threadIdx.x == 0) counters[bk] = 0;
 }
 
 template __global__ void attn_decode_kernel<1>(const bf16*, const bf16*, const bf16*, const int64_t*, int,

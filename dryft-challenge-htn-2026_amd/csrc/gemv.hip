@@ -94,34 +94,118 @@ __device__ __forceinline__ void gemv_wave_reduce(f32x4 acc[NR], float* red /* [3
   }
 }
 
-// grid (ceil(N/16), SK). partials == 0 (only with SK == 1): y[m*ldy + n] = bf16(sum);
-// otherwise fp32 ws[(s*M + m)*N + n] = sum over split s.
-template <int U>
+// Epilogue modes of gemv_kernel.
+//   GEMV_OUT      y = bf16(x.W^T)
+//   GEMV_ADD_RMS  hn = bf16(h + bf16(x.W^T)); y = bf16(bf16(hn * r) * lnw),
+//                 r = 1/sqrt(mean(hn^2) + eps) over each full row (engine.py:140-142)
+// grid (ceil(N/16), nsplit). With nsplit > 1 every split stores its fp32 partial tile and the
+// last split to arrive for a tile (per-tile counter) sums the partials in split order. In
+// GEMV_ADD_RMS the tile finisher also adds the residual and stores the tile's per-row sum of
+// squares; the last tile to finish (global counter) normalises every row.
+// Workspace (floats): partials [nsplit][M][N] | hn32 [M][N] | ss [ntiles][M].
+// Counters: [ntiles] per tile, then 1 global; zero before the launch, zero after it.
+enum { GEMV_OUT = 0, GEMV_ADD_RMS = 1 };
+
+template <int U, int MODE>
 __global__ void __launch_bounds__(GEMV_THREADS)
 gemv_kernel(const bf16* __restrict__ x, const bf16* __restrict__ W, bf16* __restrict__ y,
-            float* __restrict__ ws, int M, int N, int K, int kps, int ldy, int partials) {
+            float* __restrict__ ws, int* __restrict__ counters, int M, int N, int K, int kps,
+            const bf16* __restrict__ h, const bf16* __restrict__ lnw, bf16* __restrict__ hn,
+            float eps) {
   __shared__ float red[(GEMV_WAVES - 1) * 64 * 4];
+  __shared__ float tile[16][17];
+  __shared__ float rrow[16];
+  __shared__ int flag;
   const int n0 = blockIdx.x * 16;
   const int s = blockIdx.y;
+  const int nsplit = gridDim.y;
+  const int ntiles = gridDim.x;
   const int k0 = s * kps;
   const int k1 = min(K, k0 + kps);
   f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
   int rows[1] = {n0};
   gemv_accumulate<1, U>(x, M, K, W, rows, N, k0, k1, acc);
   gemv_wave_reduce<1>(acc, red);
-  if ((threadIdx.x >> 6) != 0) return;
   const int lane = threadIdx.x & 63;
-  const int m = lane & 15;
-  if (m >= M) return;
-  const int nb = n0 + (lane >> 4) * 4;
-  if (!partials) {
+  if (threadIdx.x < 64) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (nb + i < N) y[(size_t)m * ldy + nb + i] = f2bf(acc[0][i]);
-  } else {
+    for (int i = 0; i < 4; ++i) tile[lane & 15][(lane >> 4) * 4 + i] = acc[0][i];
+  }
+  __syncthreads();
+  // one tile element per thread: row m, column n0 + c
+  const int m = threadIdx.x >> 4, c = threadIdx.x & 15, n = n0 + c;
+  const bool mine = m < M && n < N;
+  float v = mine ? tile[m][c] : 0.f;
+  const unsigned MN = (unsigned)(M * N);
+  const rsrc_t wsr = make_rsrc(ws, (unsigned)(((MODE == GEMV_ADD_RMS) ? (size_t)nsplit * MN + MN / 2 + 1 + (size_t)ntiles * M
+                                                                       : (size_t)nsplit * MN) * 4));
+  if (nsplit > 1) {
+    if (mine) stc_f32(wsr, (unsigned)(((size_t)s * M + m) * N + n) * 4, v);
+    if (!arrive_last(counters + blockIdx.x, nsplit, &flag)) return;
+    float part[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (nb + i < N) ws[((size_t)s * M + m) * N + nb + i] = acc[0][i];
+    for (int sp = 0; sp < 16; ++sp)
+      part[sp] = (mine && sp < nsplit) ? ldc_f32(wsr, (unsigned)(((size_t)sp * M + m) * N + n) * 4) : 0.f;
+    v = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) v += part[sp];  // split order
+  }
+  if (MODE == GEMV_OUT) {
+    if (mine) y[(size_t)m * N + n] = f2bf(v);
+    return;
+  }
+  // GEMV_ADD_RMS: residual, tile sum of squares, then the last tile normalises every row.
+  // hn goes out twice: plainly (the returned tensor) and through sc1 as bf16 into the
+  // workspace (read back by the finishing workgroup).
+  const unsigned hn_off = (unsigned)((size_t)nsplit * MN * 4);          // bf16 [M][N]
+  const unsigned ss_off = hn_off + ((MN * 2 + 3) & ~3u);                 // f32 [ntiles][M]
+  float hv = 0.f;
+  if (mine) {
+    const bf16 hb = f2bf(bf2f(h[(size_t)m * N + n]) + rbf(v));
+    hv = bf2f(hb);
+    hn[(size_t)m * N + n] = hb;
+    stc_b16(wsr, hn_off + (unsigned)((size_t)m * N + n) * 2, hb);
+  }
+  float q = hv * hv;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);  // sum over the 16 columns, fixed order
+  if (c == 0 && m < M) stc_f32(wsr, ss_off + (unsigned)((size_t)blockIdx.x * M + m) * 4, q);
+  if (!arrive_last(counters + ntiles, ntiles, &flag)) return;
+  if (threadIdx.x < 16 * 16) {
+    // rows split over 16 lanes each: lane j of row m sums tiles j, j+16, ... then a 16-lane sum
+    const int mm = threadIdx.x >> 4, j = threadIdx.x & 15;
+    float t = 0.f;
+    if (mm < M)
+      for (int tl = j; tl < ntiles; tl += 16) t += ldc_f32(wsr, ss_off + (unsigned)(tl * M + mm) * 4);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (j == 0 && mm < M) rrow[mm] = rsqrt_ieee(t / (float)N + eps);
+  }
+  __syncthreads();
+  // y = bf16(bf16(hn * r) * lnw), 8 elements per 16-byte load (N % 8 == 0 here: K-side checks
+  // guarantee 16-byte rows; the scalar tail handles any remainder)
+  const bool al = ((((uintptr_t)y) | ((uintptr_t)lnw)) & 15) == 0;
+  const int nvec = (N % 8 == 0 && al) ? (int)(MN / 8) : 0;
+  for (int e = threadIdx.x; e < nvec; e += GEMV_THREADS) {
+    const u32x4 hv8 = ldc_b128(wsr, hn_off + (unsigned)e * 16);
+    const int mm = (e * 8) / N, nn = (e * 8) % N;
+    const u32x4 w8 = ld16(lnw + nn);
+    const float r = rrow[mm];
+    const unsigned hw[4] = {hv8.x, hv8.y, hv8.z, hv8.w}, ww[4] = {w8.x, w8.y, w8.z, w8.w};
+    unsigned o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned lo = f2bf(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]));
+      const unsigned hi = f2bf(rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
+      o[j] = lo | (hi << 16);
+    }
+    *(u32x4*)(y + (size_t)e * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+  for (int e = nvec * 8 + threadIdx.x; e < (int)MN; e += GEMV_THREADS) {
+    const int mm = e / N, nn = e % N;
+    const unsigned pair = ldc_u32(wsr, hn_off + ((unsigned)e * 2 & ~3u));
+    const float hx = (e & 1) ? hi_bf(pair) : lo_bf(pair);
+    y[e] = f2bf(rbf(hx * rrow[mm]) * bf2f(lnw[nn]));
   }
 }
 
@@ -156,16 +240,6 @@ gemv_silu_kernel(const bf16* __restrict__ x, const bf16* __restrict__ Wgu, bf16*
   }
 }
 
-// Sum SK fp32 partials (fixed order) -> bf16.  grid ceil(M*N/256)
-__global__ void splitk_reduce_kernel(const float* __restrict__ ws, bf16* __restrict__ y, int SK,
-                                     int MN) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
-  float a = 0.f;
-  for (int s = 0; s < SK; ++s) a += ws[(size_t)s * MN + i];
-  y[i] = f2bf(a);
-}
-
 }  // namespace dd
 
 // ------------------------------------------------------------------------------------------
@@ -186,14 +260,33 @@ int pick_splitk(int M, int N, int K) {
 
 int kps_for(int K, int sk) { return ((K + sk - 1) / sk + 31) / 32 * 32; }
 
-int launch_gemv(const void* x, const void* W, void* y, void* ws, int M, int N, int K, int sk,
-                bool partials, hipStream_t stream) {
+int gemv_nsplit(int K, int sk) {
+  const int kps = kps_for(K, sk);
+  return (K + kps - 1) / kps;
+}
+
+size_t gemv_ws_floats(int M, int N, int K, int sk, bool add_rms) {
+  const int nsplit = gemv_nsplit(K, sk);
+  size_t f = nsplit > 1 ? (size_t)nsplit * M * N : 0;
+  // add_rms: partials | hn as bf16 (rounded up to whole floats) | per-tile sums of squares
+  if (add_rms) f = (size_t)nsplit * M * N + ((size_t)M * N + 1) / 2 + (size_t)((N + 15) / 16) * M;
+  return f;
+}
+
+int launch_gemv(const void* x, const void* W, void* y, void* ws, int* counters, int M, int N,
+                int K, int sk, const void* h, const void* lnw, void* hn, float eps,
+                hipStream_t stream) {
   const int kps = kps_for(K, sk);
   const int nsplit = (K + kps - 1) / kps;
   dim3 grid((N + 15) / 16, nsplit);
-  hipLaunchKernelGGL(gemv_kernel<8>, grid, dim3(GEMV_THREADS), 0, stream, (const bf16*)x,
-                     (const bf16*)W, (bf16*)y, (float*)ws, M, N, K, kps, N,
-                     (int)(partials || nsplit > 1));
+  if (h == nullptr)
+    hipLaunchKernelGGL((gemv_kernel<8, GEMV_OUT>), grid, dim3(GEMV_THREADS), 0, stream,
+                       (const bf16*)x, (const bf16*)W, (bf16*)y, (float*)ws, counters, M, N, K,
+                       kps, nullptr, nullptr, nullptr, 0.f);
+  else
+    hipLaunchKernelGGL((gemv_kernel<8, GEMV_ADD_RMS>), grid, dim3(GEMV_THREADS), 0, stream,
+                       (const bf16*)x, (const bf16*)W, (bf16*)y, (float*)ws, counters, M, N, K,
+                       kps, (const bf16*)h, (const bf16*)lnw, (bf16*)hn, eps);
   return nsplit;
 }
 
@@ -207,26 +300,23 @@ DD_API int dd_gemv_splitk(int M, int N, int K) { return pick_splitk(M, N, K); }
 
 // Bytes of fp32 partials for a split (at least one split's worth, which the fused
 // add+norm path always uses).
+// Bytes of fp32 workspace dd_gemv needs (0 without split-K).
 DD_API size_t dd_gemv_ws_bytes(int M, int N, int K, int splitk) {
   if (splitk <= 0) splitk = pick_splitk(M, N, K);
-  const int kps = kps_for(K, splitk);
-  const int nsplit = (K + kps - 1) / kps;
-  return (size_t)(nsplit < 1 ? 1 : nsplit) * M * N * sizeof(float);
+  return gemv_ws_floats(M, N, K, splitk, false) * sizeof(float);
 }
 
+// Ints of zeroed counters dd_gemv / dd_gemv_add_rmsnorm need: one per 16-column tile + 1.
+DD_API int dd_gemv_counters(int N) { return (N + 15) / 16 + 1; }
+
 DD_API int dd_gemv(const void* x, const void* W, void* y, int M, int N, int K, int splitk, void* ws,
-                   hipStream_t stream) {
+                   int* counters, hipStream_t stream) {
   DD_REQUIRE(x && W && y && M >= 1 && M <= 16 && N >= 1 && K >= 8 && K % 8 == 0);
   DD_REQUIRE(aligned16(x) && aligned16(W));
   if (splitk <= 0) splitk = pick_splitk(M, N, K);
-  const int nsplit = (K + kps_for(K, splitk) - 1) / kps_for(K, splitk);
-  DD_REQUIRE(nsplit == 1 || ws != nullptr);
-  launch_gemv(x, W, y, ws, M, N, K, splitk, /*partials=*/false, stream);
-  if (nsplit > 1) {
-    const int MN = M * N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((MN + 255) / 256), dim3(256), 0, stream,
-                       (const float*)ws, (bf16*)y, nsplit, MN);
-  }
+  DD_REQUIRE(gemv_nsplit(K, splitk) <= 16);
+  DD_REQUIRE(gemv_nsplit(K, splitk) == 1 || (ws != nullptr && counters != nullptr));
+  launch_gemv(x, W, y, ws, counters, M, N, K, splitk, nullptr, nullptr, nullptr, 0.f, stream);
   return launch_status();
 }
 

@@ -10,13 +10,52 @@ namespace dd {
 
 constexpr int NORM_THREADS = 256;
 constexpr int NORM_WAVES = NORM_THREADS / 64;
-constexpr int NORM_MAXV = 16;  // values held per thread: N <= 16 * 256 = 4096
+constexpr int NORM_NV = 2;                        // 16-byte vectors per thread
+constexpr int NORM_MAXN = NORM_NV * 8 * NORM_THREADS;  // 4096
 
-// y = bf16(bf16(v * r) * w) for the row held in v[] (element c = tid + j*NORM_THREADS; slots
-// past N hold 0); r = 1/sqrt(sum(v^2)/N + eps)
-__device__ __forceinline__ void norm_store(const float (&v)[NORM_MAXV], int N,
-                                           const bf16* __restrict__ w, bf16* __restrict__ y,
-                                           float eps, float* red) {
+__device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
+  f[0] = lo_bf(v.x); f[1] = hi_bf(v.x); f[2] = lo_bf(v.y); f[3] = hi_bf(v.y);
+  f[4] = lo_bf(v.z); f[5] = hi_bf(v.z); f[6] = lo_bf(v.w); f[7] = hi_bf(v.w);
+}
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+  u32x4 o;
+  o.x = (unsigned)f2bf(f[0]) | ((unsigned)f2bf(f[1]) << 16);
+  o.y = (unsigned)f2bf(f[2]) | ((unsigned)f2bf(f[3]) << 16);
+  o.z = (unsigned)f2bf(f[4]) | ((unsigned)f2bf(f[5]) << 16);
+  o.w = (unsigned)f2bf(f[6]) | ((unsigned)f2bf(f[7]) << 16);
+  return o;
+}
+
+// Row normalisation of values already in registers: v[j][e] is column (tid + j*256)*8 + e
+// (columns >= N hold 0). Writes y = bf16(bf16(v * r) * w), r = 1/sqrt(sum(v^2)/N + eps).
+__device__ __forceinline__ void norm_row_vec(float (&v)[NORM_NV][8], int N,
+                                             const bf16* __restrict__ w, bf16* __restrict__ y,
+                                             float eps, float* red) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NORM_NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+  ss = block_sum<NORM_WAVES>(ss, red);
+  const float r = rsqrt_ieee(ss / (float)N + eps);
+#pragma unroll
+  for (int j = 0; j < NORM_NV; ++j) {
+    const int c8 = threadIdx.x + j * NORM_THREADS;
+    if (c8 * 8 < N) {
+      float wf[8], o[8];
+      unpack8(ld16(w + c8 * 8), wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = rbf(v[j][e] * r) * wf[e];
+      *(u32x4*)(y + c8 * 8) = pack8(o);
+    }
+  }
+}
+
+// Scalar fallback (N not a multiple of 8 or unaligned rows); N <= NORM_MAXN.
+constexpr int NORM_MAXV = NORM_MAXN / NORM_THREADS;
+__device__ __forceinline__ void norm_row_scalar(float (&v)[NORM_MAXV], int N,
+                                                const bf16* __restrict__ w, bf16* __restrict__ y,
+                                                float eps, float* red) {
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NORM_MAXV; ++j) ss += v[j] * v[j];
@@ -29,19 +68,37 @@ __device__ __forceinline__ void norm_store(const float (&v)[NORM_MAXV], int N,
   }
 }
 
+__device__ __forceinline__ bool vec_ok(int N, const void* a, const void* b, const void* c,
+                                       const void* d) {
+  return N % 8 == 0 && ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)c) | ((uintptr_t)d)) & 15) == 0;
+}
+
 // y[m] = rms(x[m]) * w                         grid (M)
 __global__ void __launch_bounds__(NORM_THREADS)
 rmsnorm_kernel(const bf16* __restrict__ x, const bf16* __restrict__ w, bf16* __restrict__ y, int N,
                float eps) {
   __shared__ float red[NORM_WAVES];
   const size_t row = blockIdx.x;
-  float v[NORM_MAXV];
+  const bf16* xr = x + row * N;
+  bf16* yr = y + row * N;
+  if (vec_ok(N, x, w, y, xr)) {
+    float v[NORM_NV][8];
 #pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int c = threadIdx.x + j * NORM_THREADS;
-    v[j] = c < N ? bf2f(x[row * N + c]) : 0.f;
+    for (int j = 0; j < NORM_NV; ++j) {
+      const int c8 = threadIdx.x + j * NORM_THREADS;
+      if (c8 * 8 < N) unpack8(ld16(xr + c8 * 8), v[j]);
+      else for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+    }
+    norm_row_vec(v, N, w, yr, eps, red);
+  } else {
+    float v[NORM_MAXV];
+#pragma unroll
+    for (int j = 0; j < NORM_MAXV; ++j) {
+      const int c = threadIdx.x + j * NORM_THREADS;
+      v[j] = c < N ? bf2f(xr[c]) : 0.f;
+    }
+    norm_row_scalar(v, N, w, yr, eps, red);
   }
-  norm_store(v, N, w, y + row * N, eps, red);
 }
 
 // hn = bf16(x + d); y = rms(hn) * w            grid (M)
@@ -50,41 +107,45 @@ add_rmsnorm_kernel(const bf16* __restrict__ x, const bf16* __restrict__ d, const
                    bf16* __restrict__ hn, bf16* __restrict__ y, int N, float eps) {
   __shared__ float red[NORM_WAVES];
   const size_t row = blockIdx.x;
-  float v[NORM_MAXV];
+  const bf16* xr = x + row * N;
+  const bf16* dr = d + row * N;
+  bf16* hr = hn + row * N;
+  bf16* yr = y + row * N;
+  if (vec_ok(N, xr, dr, hr, yr) && ((((uintptr_t)w) & 15) == 0)) {
+    u32x4 xa[NORM_NV], da[NORM_NV];
 #pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int c = threadIdx.x + j * NORM_THREADS;
-    v[j] = 0.f;
-    if (c < N) {
-      const bf16 s = f2bf(bf2f(x[row * N + c]) + bf2f(d[row * N + c]));
-      hn[row * N + c] = s;
-      v[j] = bf2f(s);
+    for (int j = 0; j < NORM_NV; ++j) {  // all loads first
+      const int c8 = threadIdx.x + j * NORM_THREADS;
+      const bool ok = c8 * 8 < N;
+      xa[j] = ok ? ld16(xr + c8 * 8) : u32x4{0u, 0u, 0u, 0u};
+      da[j] = ok ? ld16(dr + c8 * 8) : u32x4{0u, 0u, 0u, 0u};
     }
-  }
-  norm_store(v, N, w, y + row * N, eps, red);
-}
-
-// Split-K epilogue: hn = bf16(h + bf16(sum_s ws[s])); y = rms(hn) * w      grid (M)
-__global__ void __launch_bounds__(NORM_THREADS)
-reduce_add_rmsnorm_kernel(const float* __restrict__ ws, int SK, const bf16* __restrict__ h,
-                          const bf16* __restrict__ w, bf16* __restrict__ hn, bf16* __restrict__ y,
-                          int M, int N, float eps) {
-  __shared__ float red[NORM_WAVES];
-  const size_t row = blockIdx.x;
-  float v[NORM_MAXV];
+    float v[NORM_NV][8];
 #pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int c = threadIdx.x + j * NORM_THREADS;
-    v[j] = 0.f;
-    if (c < N) {
-      float a = 0.f;
-      for (int s = 0; s < SK; ++s) a += ws[((size_t)s * M + row) * N + c];
-      const bf16 t = f2bf(bf2f(h[row * N + c]) + rbf(a));
-      hn[row * N + c] = t;
-      v[j] = bf2f(t);
+    for (int j = 0; j < NORM_NV; ++j) {
+      float a[8], b[8];
+      unpack8(xa[j], a);
+      unpack8(da[j], b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = rbf(a[e] + b[e]);
+      const int c8 = threadIdx.x + j * NORM_THREADS;
+      if (c8 * 8 < N) *(u32x4*)(hr + c8 * 8) = pack8(v[j]);
     }
+    norm_row_vec(v, N, w, yr, eps, red);
+  } else {
+    float v[NORM_MAXV];
+#pragma unroll
+    for (int j = 0; j < NORM_MAXV; ++j) {
+      const int c = threadIdx.x + j * NORM_THREADS;
+      v[j] = c < N ? rbf(bf2f(xr[c]) + bf2f(dr[c])) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < NORM_MAXV; ++j) {
+      const int c = threadIdx.x + j * NORM_THREADS;
+      if (c < N) hr[c] = f2bf(v[j]);
+    }
+    norm_row_scalar(v, N, w, yr, eps, red);
   }
-  norm_store(v, N, w, y + row * N, eps, red);
 }
 
 // h[m] = embed[tok[m]]; y = rms(h) * w           grid (M)
@@ -99,18 +160,38 @@ embed_rmsnorm_kernel(const int64_t* __restrict__ tok, const bf16* __restrict__ e
     if (threadIdx.x == 0 && err != nullptr) atomicOr(err, 1);
     t = 0;
   }
-  float v[NORM_MAXV];
+  const bf16* er = embed + (size_t)t * N;
+  bf16* hr = h + row * N;
+  bf16* yr = y + row * N;
+  if (vec_ok(N, er, hr, yr, w)) {
+    u32x4 ea[NORM_NV];
 #pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int c = threadIdx.x + j * NORM_THREADS;
-    v[j] = 0.f;
-    if (c < N) {
-      const bf16 s = embed[(size_t)t * N + c];
-      h[row * N + c] = s;
-      v[j] = bf2f(s);
+    for (int j = 0; j < NORM_NV; ++j) {
+      const int c8 = threadIdx.x + j * NORM_THREADS;
+      ea[j] = c8 * 8 < N ? ld16(er + c8 * 8) : u32x4{0u, 0u, 0u, 0u};
     }
+    float v[NORM_NV][8];
+#pragma unroll
+    for (int j = 0; j < NORM_NV; ++j) {
+      unpack8(ea[j], v[j]);
+      const int c8 = threadIdx.x + j * NORM_THREADS;
+      if (c8 * 8 < N) *(u32x4*)(hr + c8 * 8) = ea[j];
+    }
+    norm_row_vec(v, N, w, yr, eps, red);
+  } else {
+    float v[NORM_MAXV];
+#pragma unroll
+    for (int j = 0; j < NORM_MAXV; ++j) {
+      const int c = threadIdx.x + j * NORM_THREADS;
+      v[j] = c < N ? bf2f(er[c]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < NORM_MAXV; ++j) {
+      const int c = threadIdx.x + j * NORM_THREADS;
+      if (c < N) hr[c] = f2bf(v[j]);
+    }
+    norm_row_scalar(v, N, w, yr, eps, red);
   }
-  norm_store(v, N, w, y + row * N, eps, red);
 }
 
 // out[m][n] = bf16(bf16(silu(g)) * u) with [g | u] = gu[m]      grid (ceil(M*I/256))
@@ -134,7 +215,7 @@ using namespace dd;
 
 DD_API int dd_rmsnorm(const void* x, const void* w, void* y, int M, int N, float eps,
                       hipStream_t stream) {
-  DD_REQUIRE(x && w && y && M >= 1 && N >= 1 && N <= NORM_MAXV * NORM_THREADS);
+  DD_REQUIRE(x && w && y && M >= 1 && N >= 1 && N <= NORM_MAXN);
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, stream, (const bf16*)x,
                      (const bf16*)w, (bf16*)y, N, eps);
   return launch_status();
@@ -142,30 +223,33 @@ DD_API int dd_rmsnorm(const void* x, const void* w, void* y, int M, int N, float
 
 DD_API int dd_add_rmsnorm(const void* x, const void* d, const void* w, void* hn, void* y, int M,
                           int N, float eps, hipStream_t stream) {
-  DD_REQUIRE(x && d && w && hn && y && M >= 1 && N >= 1 && N <= NORM_MAXV * NORM_THREADS);
+  DD_REQUIRE(x && d && w && hn && y && M >= 1 && N >= 1 && N <= NORM_MAXN);
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, stream, (const bf16*)x,
                      (const bf16*)d, (const bf16*)w, (bf16*)hn, (bf16*)y, N, eps);
   return launch_status();
 }
 
+DD_API size_t dd_gemv_add_rmsnorm_ws_bytes(int M, int N, int K, int splitk) {
+  if (splitk <= 0) splitk = pick_splitk(M, N, K);
+  return gemv_ws_floats(M, N, K, splitk, true) * sizeof(float);
+}
+
 DD_API int dd_gemv_add_rmsnorm(const void* x, const void* W, const void* h, const void* lnw,
                                void* hn, void* y, int M, int N, int K, float eps, int splitk,
-                               void* ws, hipStream_t stream) {
-  DD_REQUIRE(x && W && h && lnw && hn && y && ws);
-  DD_REQUIRE(M >= 1 && M <= 16 && N >= 1 && N <= NORM_MAXV * NORM_THREADS && K >= 8 && K % 8 == 0);
+                               void* ws, int* counters, hipStream_t stream) {
+  DD_REQUIRE(x && W && h && lnw && hn && y && ws && counters);
+  DD_REQUIRE(M >= 1 && M <= 16 && N >= 1 && K >= 8 && K % 8 == 0);
   DD_REQUIRE(aligned16(x) && aligned16(W));
   if (splitk <= 0) splitk = pick_splitk(M, N, K);
-  const int got = launch_gemv(x, W, nullptr, ws, M, N, K, splitk, /*partials=*/true, stream);
-  hipLaunchKernelGGL(reduce_add_rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, stream,
-                     (const float*)ws, got, (const bf16*)h, (const bf16*)lnw, (bf16*)hn, (bf16*)y,
-                     M, N, eps);
+  DD_REQUIRE(gemv_nsplit(K, splitk) <= 16);
+  launch_gemv(x, W, y, ws, counters, M, N, K, splitk, h, lnw, hn, eps, stream);
   return launch_status();
 }
 
 DD_API int dd_embed_rmsnorm(const int64_t* tok, const void* embed, int V, const void* w, void* h,
                             void* y, int M, int N, float eps, int* err, hipStream_t stream) {
   DD_REQUIRE(tok && embed && w && h && y && M >= 1 && V >= 1 && N >= 1 &&
-             N <= NORM_MAXV * NORM_THREADS);
+             N <= NORM_MAXN);
   hipLaunchKernelGGL(embed_rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, stream, tok,
                      (const bf16*)embed, V, (const bf16*)w, (bf16*)h, (bf16*)y, N, eps, err);
   return launch_status();

@@ -11,8 +11,8 @@
 //   out[d+64] = bf16(bf16(n[d+64] * cos[d+64]) + bf16(n[d] * sin[d+64]))
 // v is copied bit for bit.
 //
-// One workgroup (4 waves) per token; wave w handles heads w, w+4, ...; lane l holds dims l and
-// l+64, i.e. exactly one rotate-half pair, so RoPE needs no data exchange.
+// grid (tokens, ceil(heads / 4)): each of the 4 waves of a workgroup handles one head; lane l
+// holds dims l and l+64, i.e. exactly one rotate-half pair, so RoPE needs no data exchange.
 #include "common.h"
 
 namespace dd {
@@ -42,14 +42,15 @@ qkv_post_decode_kernel(const bf16* __restrict__ qkv, const bf16* __restrict__ qn
   const size_t cb = (size_t)position * HD;
   const float c1 = bf2f(cos_t[cb + lane]), c2 = bf2f(cos_t[cb + HALF + lane]);
   const float s1 = bf2f(sin_t[cb + lane]), s2 = bf2f(sin_t[cb + HALF + lane]);
-  for (int h = wave; h < NH + 2 * NKV; h += QKV_THREADS / 64) {
+  const int h = blockIdx.y * (QKV_THREADS / 64) + wave;
+  if (h < NH + 2 * NKV) {
     const bf16* base = row + h * HD;
     const bf16 x1b = base[lane], x2b = base[HALF + lane];
     if (h >= NH + NKV) {  // v: straight copy into the cache
       bf16* vo = vc + (((size_t)b * NKV + (h - NH - NKV)) * cap + position) * HD;
       vo[lane] = x1b;
       vo[HALF + lane] = x2b;
-      continue;
+      return;
     }
     const float f1 = bf2f(x1b), f2 = bf2f(x2b);
     const float ss = wave_sum(f1 * f1 + f2 * f2);
@@ -85,7 +86,8 @@ DD_API int dd_qkv_post_decode(const void* qkv, const void* qn, const void* kn, c
   DD_REQUIRE(qkv && qn && kn && cos_t && sin_t && pos && q && kc && vc);
   DD_REQUIRE(HD == 128 && B >= 1 && S >= 1 && NKV >= 1 && NH >= NKV && NH % NKV == 0);
   DD_REQUIRE(cap >= 1 && rope_rows >= 1 && (pos_stride == 0 || pos_stride == 1));
-  hipLaunchKernelGGL(qkv_post_decode_kernel, dim3(B * S), dim3(QKV_THREADS), 0, stream,
+  const int heads = NH + 2 * NKV;
+  hipLaunchKernelGGL(qkv_post_decode_kernel, dim3(B * S, (heads + 3) / 4), dim3(QKV_THREADS), 0, stream,
                      (const bf16*)qkv, (const bf16*)qn, (const bf16*)kn, (const bf16*)cos_t,
                      (const bf16*)sin_t, pos, pos_stride, (bf16*)q, (bf16*)kc, (bf16*)vc, S, NH,
                      NKV, cap, rope_rows, eps, err);

@@ -74,10 +74,12 @@ class HipOps:
         self.err = torch.zeros(1, dtype=torch.int32, device=e.dev)
 
     # ---------------------------------------------------------------- helpers
-    def _attn_counters(self, n, dev):
+    def _zeroed_counters(self, n, dev):
+        """Zeroed int32 counters shared by every call on this stream (the kernels leave them
+        zero). Allocated once, outside graph capture, and grown only when a larger op needs it."""
         c = self._counters
         if c is None or c.numel() < n or c.device != dev:
-            self._counters = torch.zeros(max(n, 256), dtype=torch.int32, device=dev)
+            self._counters = torch.zeros(max(n, 16384), dtype=torch.int32, device=dev)
         return self._counters
 
     def _gemv_ok(self, x, w):
@@ -127,11 +129,12 @@ class HipOps:
         N = w.shape[0]
         out = torch.empty((M, N), dtype=x.dtype, device=x.device)
         sk = self.L.dd_gemv_splitk(M, N, K)
-        ws = None
-        if sk > 1:
-            ws = torch.empty(self.L.dd_gemv_ws_bytes(M, N, K, sk) // 4, dtype=torch.float32,
-                             device=x.device)
-        check(self.L.dd_gemv(_ptr(x), _ptr(w), _ptr(out), M, N, K, sk, _ptr(ws),
+        ws = cnt = None
+        nbytes = self.L.dd_gemv_ws_bytes(M, N, K, sk)
+        if nbytes:
+            ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
+            cnt = self._zeroed_counters(self.L.dd_gemv_counters(N), x.device)
+        check(self.L.dd_gemv(_ptr(x), _ptr(w), _ptr(out), M, N, K, sk, _ptr(ws), _ptr(cnt),
                              _stream(x.device)), "dd_gemv")
         return out
 
@@ -152,13 +155,14 @@ class HipOps:
         M, K = x.shape
         N = w.shape[0]
         sk = self.L.dd_gemv_splitk(M, N, K)
-        ws = torch.empty(self.L.dd_gemv_ws_bytes(M, N, K, sk) // 4, dtype=torch.float32,
-                         device=x.device)
+        ws = torch.empty(self.L.dd_gemv_add_rmsnorm_ws_bytes(M, N, K, sk) // 4,
+                         dtype=torch.float32, device=x.device)
+        cnt = self._zeroed_counters(self.L.dd_gemv_counters(N), x.device)
         hn = torch.empty_like(h)
         y = torch.empty_like(h)
         check(self.L.dd_gemv_add_rmsnorm(_ptr(x), _ptr(w), _ptr(h), _ptr(lnw), _ptr(hn), _ptr(y),
-                                         M, N, K, self.e.eps, sk, _ptr(ws), _stream(x.device)),
-              "dd_gemv_add_rmsnorm")
+                                         M, N, K, self.e.eps, sk, _ptr(ws), _ptr(cnt),
+                                         _stream(x.device)), "dd_gemv_add_rmsnorm")
         return hn, y
 
     # ---------------------------------------------------------------- attention block
@@ -185,7 +189,7 @@ class HipOps:
         out = torch.empty((B * W, e.nh * e.hd), dtype=q.dtype, device=q.device)
         ws = torch.empty(max(1, self.L.dd_attn_ws_bytes(B, W, e.nh, e.nkv, e.hd, cap, chunk) // 4),
                          dtype=torch.float32, device=q.device)
-        counters = self._attn_counters(B * e.nkv, q.device)
+        counters = self._zeroed_counters(B * e.nkv, q.device)
         pos_stride = 1 if pos.numel() > 1 else 0
         check(self.L.dd_attn_decode(_ptr(q.contiguous()), _ptr(kc), _ptr(vc), _ptr(pos), pos_stride,
                                     _ptr(out), _ptr(ws), _ptr(counters), B, W, e.nh, e.nkv, e.hd,
@@ -207,9 +211,12 @@ class HipOps:
     def argmax_(self, logits, tok, pos=None):
         """tok[:] = logits.argmax(-1); pos += 1 when given (engine.py:503, 539-540)."""
         M, V = logits.shape
+        ws = torch.empty(self.L.dd_argmax_ws_bytes(M, V) // 4, dtype=torch.float32,
+                         device=logits.device)
+        cnt = self._zeroed_counters(M, logits.device)
         check(self.L.dd_argmax(_ptr(logits.contiguous()), M, V, _ptr(tok), _ptr(pos),
-                               0 if pos is None else pos.numel(), _stream(logits.device)),
-              "dd_argmax")
+                               0 if pos is None else pos.numel(), _ptr(ws), _ptr(cnt),
+                               _stream(logits.device)), "dd_argmax")
         return tok
 
     def embed_rms(self, tokens, embed, w):

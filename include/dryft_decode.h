@@ -18,6 +18,10 @@
  *  - ``err`` (optional, may be NULL) is a device int that kernels OR flags into instead of
  *    faulting: 1 = token id out of range (row 0 used), 2 = position outside cache/rope table
  *    (row skipped).
+ *  - ``counters`` are caller-owned device ints that must be zero before the first call; every
+ *    call leaves them zero again (the last workgroup to arrive resets them), so one zeroed
+ *    buffer serves any number of calls on one stream. Calls that overlap in time must not share
+ *    counters or workspaces.
  */
 #ifndef DRYFT_DECODE_H
 #define DRYFT_DECODE_H
@@ -44,24 +48,29 @@ int dd_add_rmsnorm(const void* x, const void* d, const void* w, void* hn, void* 
                    float eps, hipStream_t stream);
 
 /* y[M,N] = x[M,K] . W[N,K]^T (bf16 out, fp32 accumulate), 1 <= M <= 16, K % 8 == 0,
- * x and W 16-byte aligned. splitk <= 0 picks the library's choice (dd_gemv_splitk); when the
- * split is > 1, ws must hold split * M * N floats (dd_gemv_ws_bytes).
+ * x and W 16-byte aligned. splitk <= 0 picks the library's choice (dd_gemv_splitk); with more
+ * than one split, ws must hold dd_gemv_ws_bytes and counters dd_gemv_counters(N) zeroed ints
+ * (the split-K sum happens in the same launch).
  * Replaces TritonOps.linear (fused.py:989-1014; kernels fused.py:568-628), reference
  * _TorchOps.linear = F.linear (engine.py:131-132). */
 int dd_gemv(const void* x, const void* W, void* y, int M, int N, int K, int splitk, void* ws,
-            hipStream_t stream);
+            int* counters, hipStream_t stream);
 
 /* The split-K factor dd_gemv / dd_gemv_add_rmsnorm use for this shape when splitk <= 0.
  * Replaces the shape-keyed tile table GEMM_CFG (fused.py:711-718, 773-789). */
 int dd_gemv_splitk(int M, int N, int K);
 size_t dd_gemv_ws_bytes(int M, int N, int K, int splitk);
+int dd_gemv_counters(int N);
 
-/* hn = bf16(h + bf16(x . W^T)); y = rmsnorm(hn) * lnw (N <= 4096).
+/* hn = bf16(h + bf16(x . W^T)); y = rmsnorm(hn) * lnw, in one launch (split-K partials, the
+ * residual and the row norm are finished by the last workgroups to arrive).
+ * ws: dd_gemv_add_rmsnorm_ws_bytes; counters: dd_gemv_counters(N) zeroed ints.
  * Replaces TritonOps.linear_add_norm (fused.py:1034-1059; kernels fused.py:568-618, 685-709),
- * reference _TorchOps.linear_add_norm (engine.py:140-142). ws as for dd_gemv (always used). */
+ * reference _TorchOps.linear_add_norm (engine.py:140-142). */
 int dd_gemv_add_rmsnorm(const void* x, const void* W, const void* h, const void* lnw, void* hn,
                         void* y, int M, int N, int K, float eps, int splitk, void* ws,
-                        hipStream_t stream);
+                        int* counters, hipStream_t stream);
+size_t dd_gemv_add_rmsnorm_ws_bytes(int M, int N, int K, int splitk);
 
 /* out[M,I] = bf16(bf16(silu(g)) * u), [g | u] = x . Wgu^T, Wgu = [gate; up] of shape [2I, K].
  * Replaces TritonOps.gate_up_silu (fused.py:1016-1032; kernel fused.py:631-682), reference
@@ -103,10 +112,11 @@ int dd_embed_rmsnorm(const int64_t* tok, const void* embed, int V, const void* w
                      void* y, int M, int N, float eps, int* err, hipStream_t stream);
 
 /* tok[m] = argmax(logits[m]) (first index on ties, NaN largest); then pos[i] += 1 for
- * i < npos when pos is not NULL.
+ * i < npos when pos is not NULL. ws: dd_argmax_ws_bytes; counters: M zeroed ints.
  * Replaces logits.argmax(-1) and st.pos.add_(1) (engine.py:503, 538-540). */
-int dd_argmax(const void* logits, int M, int V, int64_t* tok, int64_t* pos, int npos,
-              hipStream_t stream);
+int dd_argmax(const void* logits, int M, int V, int64_t* tok, int64_t* pos, int npos, void* ws,
+              int* counters, hipStream_t stream);
+size_t dd_argmax_ws_bytes(int M, int V);
 
 /* Measurement helper, no counterpart in the reference: streams `bytes` from p (16-byte words,
  * nontemporal loads) with the given launch shape; used to measure the achievable HBM read

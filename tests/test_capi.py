@@ -33,14 +33,16 @@ def test_validation_rejects_without_launch():
     L = dryft_amd.lib()
     INVALID = 1
     # null pointers
-    assert L.dd_gemv(None, None, None, 1, 16, 64, 1, None, None) == INVALID
+    assert L.dd_gemv(None, None, None, 1, 16, 64, 1, None, None, None) == INVALID
     assert L.dd_rmsnorm(None, None, None, 1, 16, 1e-6, None) == INVALID
     # shape limits checked before any pointer is used (fake, never-dereferenced addresses)
     fake = ctypes.c_void_p(0x1000)
-    assert L.dd_gemv(fake, fake, fake, 17, 16, 64, 1, None, None) == INVALID   # M > 16
-    assert L.dd_gemv(fake, fake, fake, 1, 16, 60, 1, None, None) == INVALID    # K % 8
-    assert L.dd_gemv(ctypes.c_void_p(0x1008), fake, fake, 1, 16, 64, 1, None, None) == INVALID
+    assert L.dd_gemv(fake, fake, fake, 17, 16, 64, 1, None, None, None) == INVALID   # M > 16
+    assert L.dd_gemv(fake, fake, fake, 1, 16, 60, 1, None, None, None) == INVALID    # K % 8
+    assert L.dd_gemv(ctypes.c_void_p(0x1008), fake, fake, 1, 16, 64, 1, None, None, None) == INVALID
+    assert L.dd_gemv(fake, fake, fake, 1, 16, 4096, 4, None, None, None) == INVALID  # split, no ws
     assert L.dd_rmsnorm(fake, fake, fake, 1, 5000, 1e-6, None) == INVALID    # N > 4096
+    assert L.dd_argmax(fake, 2, 100, fake, None, 0, None, None, None) == INVALID  # no ws
     assert L.dd_qkv_post_decode(fake, fake, fake, fake, fake, 64, fake, 0, fake, fake, fake,
                                 1, 1, 32, 8, 64, 128, 1e-6, None, None) == INVALID   # HD != 128
     assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
@@ -61,7 +63,11 @@ def test_host_side_sizing():
     assert L.dd_gemv_splitk(16, 151936, 2560) == 1
     for M, N, K in ((16, 2560, 4096), (1, 6144, 2560), (3, 64, 64)):
         sk = L.dd_gemv_splitk(M, N, K)
-        assert L.dd_gemv_ws_bytes(M, N, K, sk) >= max(sk, 1) * M * N * 4
+        assert L.dd_gemv_ws_bytes(M, N, K, sk) == (sk * M * N * 4 if sk > 1 else 0)
+        # partials | hn as bf16 (rounded up to whole floats) | per-tile sums of squares
+        assert L.dd_gemv_add_rmsnorm_ws_bytes(M, N, K, sk) == 4 * (sk * M * N + (M * N + 1) // 2 + -(-N // 16) * M)
+        assert L.dd_gemv_counters(N) == -(-N // 16) + 1
+    assert L.dd_argmax_ws_bytes(16, 151936) == 16 * 38 * 2 * 4
     # attention: chunk multiple of 128, workspace covers every split of every row
     for B, cap in ((1, 640), (16, 3072), (16, 8192)):
         c = L.dd_attn_chunk(B, 8, cap)

@@ -78,8 +78,11 @@ def test_known_gemv_splitk_equals_direct(small):
     xg, wg = x.to(BF).cuda(), w.to(BF).cuda()
     y = torch.empty(M, N, dtype=BF, device="cuda")
     ws = torch.empty(2 * M * N, dtype=torch.float32, device="cuda")
+    cnt = torch.zeros(L.dd_gemv_counters(N), dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    assert L.dd_gemv(xg.data_ptr(), wg.data_ptr(), y.data_ptr(), M, N, K, 2, ws.data_ptr(), st) == 0
+    assert L.dd_gemv(xg.data_ptr(), wg.data_ptr(), y.data_ptr(), M, N, K, 2, ws.data_ptr(),
+                     cnt.data_ptr(), st) == 0
+    assert not cnt.any()                                  # counters left at zero
     assert torch.equal(y.float().cpu(), exp)
 
 
