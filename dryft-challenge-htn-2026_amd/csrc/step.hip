@@ -1,0 +1,1007 @@
+// Persistent decode step for MI355X (gfx950): one launch runs a whole Qwen3-shape decode step.
+//
+// Grid: one 512-thread workgroup per CU, all co-resident. The step is a fixed list of phases:
+//   0            embedding gather  h = embed[tok], per-64-column sums of squares
+//   per layer    QKV GEMV (+ per-head q/k RMSNorm, RoPE, K/V cache write)
+//                split-KV attention (+ log-sum-exp combine)
+//                O GEMV (+ residual, sums of squares)
+//                gate/up GEMV (+ SiLU x up)
+//                down GEMV (+ residual, sums of squares)
+//   last         lm_head GEMV (+ logits, argmax, pos += 1)
+// with a grid barrier between phases.
+//
+// GEMV phases stream weights that were re-laid out once into "MFMA tile order" (dd_tile_weight):
+// the A operand of one v_mfma_f32_16x16x32_bf16 (16 rows x 32 k) is one contiguous 1 KB block
+// in lane order, so every weight load instruction of a wave reads 1 KB contiguous (a 16-row x
+// 64-byte pattern only reaches ~70% of the HBM bandwidth on MI355X). NR tiles that share a group
+// of rows sit next to each other per 32-k step ("step" = NR blocks). Each workgroup owns a
+// contiguous range of steps (stream-K): equal bytes per CU; a row group cut between workgroups
+// is finished by the last of its contributors to arrive (partials in split order: deterministic).
+// The activation operand x of a phase is staged once into LDS per workgroup (only the k window
+// that workgroup needs), with the RMSNorm of the residual stream applied on the way in.
+//
+// Barriers are split: a workgroup arrives (after its stores completed), then issues the weight
+// loads of the next phase, then waits -- the HBM stream keeps going through the barrier.
+//
+// Cross-workgroup data inside the launch moves with sc1 stores/loads (served at the device
+// coherence point, see common.h); every spin has a wall-clock timeout that raises a flag
+// instead of hanging.
+#include "common.h"
+
+namespace dd {
+namespace st {
+
+constexpr int NWAVE = 8;
+constexpr int NTHR = NWAVE * 64;
+constexpr int HD = 128;
+constexpr int SSG = 64;      // residual columns per sum-of-squares group (O/down row group)
+constexpr int MAXM = 16;
+constexpr int BATCH = 8;     // weight blocks (1 KB each) per prefetch batch per wave
+
+enum : int { F_WQKV = 0, F_WO, F_WGU, F_WD, F_LN1, F_LN2, F_QN, F_KN, F_KC, F_VC, NFIELD = 16 };
+
+// counters (ints)
+constexpr int C_BAR = 0;          // [0] top, [64 * (1 + xcd)] per XCD
+constexpr int C_EXIT = 640;
+constexpr int C_GROUP = 1024;     // per row-group fixup counters
+constexpr int C_ATT = C_GROUP + 8192;
+constexpr int C_AM = C_ATT + 512;
+constexpr int C_TOTAL = C_AM + 64;
+
+// error flags
+constexpr int E_TOKEN = 1, E_POS = 2, E_TIMEOUT = 4, E_GEOM = 8;
+
+// tiles per row group of each GEMV phase (log2)
+constexpr int LNR_QKV = 3, LNR_O = 2, LNR_GU = 1, LNR_D = 2, LNR_LM = 1;
+
+struct Args {
+  const int64_t* layers;             // [L][NFIELD] device pointers
+  const bf16* embed;                 // [V][H] natural layout (gather)
+  const bf16* lm_t;                  // lm_head, tiled with NR = 2
+  const bf16* fnorm;                 // final RMSNorm weight [H]
+  const bf16* cos_t;
+  const bf16* sin_t;
+  int64_t* tok;                      // [M] in: this step's tokens, out: next tokens
+  int64_t* pos;                      // [M] per-row positions, += 1 at the end
+  bf16* h;                           // [M][H] residual stream
+  bf16* qbuf;                        // [M][NH][HD]
+  bf16* attn;                        // [M][NH*HD]
+  bf16* mbuf;                        // [M][I]
+  bf16* logits;                      // [M][V]
+  float* ws;
+  int* ctr;
+  int* err;
+  int L, M, H, NH, NKV, I, V, cap, rope_rows, chunk;
+  float eps;
+  int phase_begin, phase_end;
+  unsigned off_ss, off_part, off_att, off_am;   // workspace offsets (floats)
+  unsigned ws_floats;
+};
+
+struct Geo {                         // one GEMV phase for this workgroup
+  const bf16* W;
+  int lnr, nk, ngroups, S, s0, s1;
+};
+
+__device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr) {
+  Geo g;
+  g.W = W;
+  g.lnr = lnr;
+  g.nk = K >> 5;
+  g.ngroups = rows >> (4 + lnr);
+  g.S = g.ngroups * g.nk;
+  g.s0 = (int)((long long)g.S * blockIdx.x / gridDim.x);
+  g.s1 = (int)((long long)g.S * (blockIdx.x + 1) / gridDim.x);
+  return g;
+}
+
+// workgroup owning global step s
+__device__ __forceinline__ int wg_of_step(const Geo& g, int s) {
+  return (int)((((long long)s + 1) * gridDim.x - 1) / g.S);
+}
+
+// first step of workgroup c's range (ranges of workgroups between two owners may be empty)
+__device__ __forceinline__ int step0_of(const Geo& g, int c) {
+  return (int)((long long)g.S * c / gridDim.x);
+}
+
+// Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks).
+template <int NR>
+__device__ __forceinline__ void issue_batch(const Geo& g, int j0, u32x4 (&buf)[BATCH]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int b = 0; b < BATCH; ++b) {
+    const int u = b / NR, t = b % NR;
+    const int s = g.s0 + wave + NWAVE * (j0 + u);
+    buf[b] = s < g.s1 ? ld16_stream(g.W + (((size_t)s * NR + t) << 9) + lane * 8)
+                      : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// GEMV phases carve their LDS out of one region: per-wave partial tiles (NR x 8 KB), the
+// reduced group tile, then the staged activation window.
+constexpr int GBUF = 112 * 1024;
+constexpr int RES_BYTES = 8 * 16 * (MAXM + 1) * 4;
+__host__ __device__ constexpr int x_capacity(int NR) { return GBUF - NR * NWAVE * 256 * 4 - RES_BYTES; }
+
+struct Shared {
+  union {
+    unsigned char g[GBUF];                    // GEMV phases (see GemvLds)
+    struct {                                  // attention
+      bf16 v[NWAVE][32][HD + 8];
+      float mrg[NWAVE][16][HD];
+    } a;
+  } u;
+  float rs[MAXM];                             // per-row 1/rms of the staged x
+  float ms[NWAVE][16];
+  float ls[NWAVE][16];
+  float bestv[MAXM];
+  int besti[MAXM];
+  int flag;
+  int bail;                                   // a barrier wait timed out: stop waiting
+  int xrs;                                    // staged x row stride (bytes)
+  int xksf, xnw;                              // staged window: first k-step, width
+  int units[MAXM + 1];                        // attention unit prefix sums
+};
+
+// ---------------------------------------------------------------------------------------------
+template <int NR>
+struct GemvLds {
+  float (*red)[NR][256];                      // [NWAVE][NR][256]
+  float (*res)[MAXM + 1];                     // [NR*16][MAXM+1]
+  unsigned char* x;
+  __device__ explicit GemvLds(Shared& sh)
+      : red((float(*)[NR][256])sh.u.g),
+        res((float(*)[MAXM + 1])(sh.u.g + NR * NWAVE * 256 * 4)),
+        x(sh.u.g + NR * NWAVE * 256 * 4 + RES_BYTES) {}
+};
+
+// barrier (split)
+__device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  if (threadIdx.x == 0) {
+    const int xcd = blockIdx.x & 7;
+    const unsigned per = (unsigned)(gridDim.x >> 3);
+    const unsigned old = __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR + 64 * (1 + xcd), 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == epoch * per - 1)
+      __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epoch) {
+  if (threadIdx.x == 0 && !sh.bail) {
+    const unsigned long long t0 = wall_clock64();
+    while (__hip_atomic_load((unsigned*)a.ctr + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+           epoch * 8) {
+      __builtin_amdgcn_s_sleep(2);
+      if (wall_clock64() - t0 > 20000000ull) {  // 200 ms: report, stop waiting from now on
+        atomicOr(a.err, E_TIMEOUT);
+        sh.bail = 1;
+        break;
+      }
+    }
+  }
+  __builtin_amdgcn_s_barrier();
+}
+
+// ---------------------------------------------------------------------------------------------
+// activation staging: x window [ksf, ksf + nw) (cyclic over nk k-steps) of an [M][K] source into
+// LDS rows of stride xrs bytes. NORM: x = bf16(bf16(h * r[m]) * lnw[k]) with r from the ss groups.
+__device__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g, int K,
+                        const bf16* src, const bf16* lnw) {
+  const int M = a.M;
+  int ksf = 0, nw = 0;
+  if (g.s1 > g.s0) {
+    ksf = g.s0 % g.nk;
+    nw = min(g.s1 - g.s0, g.nk);
+  }
+  const int xrs = nw * 64 + 16;
+  if (lnw != nullptr && threadIdx.x < 64) {
+    // r[m] = 1/sqrt(sum_g ss[g][m] / H + eps); lanes 0..15 one row each, groups in order
+    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
+    const int m = threadIdx.x;
+    if (m < M) {
+      float t = 0.f;
+      for (int q = 0; q < a.H / SSG; ++q) t += ldc_f32(ssr, (unsigned)(q * MAXM + m) * 4);
+      sh.rs[m] = rsqrt_ieee(t / (float)a.H + a.eps);
+    }
+  }
+  if (threadIdx.x == 0) {
+    sh.xrs = xrs;
+    sh.xksf = ksf;
+    sh.xnw = nw;
+  }
+  __syncthreads();
+  const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
+  const int items = M * nw * 4;
+  for (int it = threadIdx.x; it < items; it += NTHR) {
+    const int m = it / (nw * 4);
+    const int rem = it - m * nw * 4;
+    const int w = rem >> 2, e = rem & 3;
+    int ks = ksf + w;
+    if (ks >= g.nk) ks -= g.nk;
+    const int k = ks * 32 + e * 8;
+    u32x4 v = ldc_b128(sr, (unsigned)((size_t)m * K + k) * 2);
+    if (lnw != nullptr) {
+      const u32x4 wv = ld16(lnw + k);
+      const float r = sh.rs[m];
+      const unsigned hw[4] = {v.x, v.y, v.z, v.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      unsigned o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned lo = f2bf(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]));
+        const unsigned hi = f2bf(rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
+        o[j] = lo | (hi << 16);
+      }
+      v = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    *(u32x4*)(xb + m * xrs + w * 64 + e * 16) = v;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------
+// GEMV epilogues. `res[row][m]` holds the fp32 sums of the group's NR*16 weight rows.
+enum { EPI_QKV = 0, EPI_RES = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
+
+__device__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int head) {
+  // head < NH: q head; < NH+NKV: k head; else v head. 128 rows = the head's 128 dims.
+  const int M = a.M;
+  const int64_t* lp = a.layers + (size_t)layer * NFIELD;
+  const bf16* qn = (const bf16*)lp[F_QN];
+  const bf16* kn = (const bf16*)lp[F_KN];
+  bf16* kc = (bf16*)lp[F_KC];
+  bf16* vc = (bf16*)lp[F_VC];
+  const int t = threadIdx.x;
+  const int m = t >> 5, j = t & 31;        // token m, dims {j, j+32, j+64, j+96}
+  const bool act = m < M;
+  int64_t p = act ? a.pos[m] : 0;
+  const bool pok = p >= 0 && p < a.cap && p < a.rope_rows;
+  if (act && !pok && j == 0) atomicOr(a.err, E_POS);
+  float x[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) x[q] = act ? rbf(res[j + 32 * q][m]) : 0.f;
+  const int NKV = a.NKV, NH = a.NH;
+  if (head >= NH + NKV) {
+    if (act && pok) {
+      const rsrc_t vr = make_rsrc(vc, (unsigned)((size_t)M * NKV * a.cap * HD * 2));
+      const size_t base = (((size_t)m * NKV + (head - NH - NKV)) * a.cap + p) * HD;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) stc_b16(vr, (unsigned)((base + j + 32 * q) * 2), f2bf(x[q]));
+    }
+    return;
+  }
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);   // 32 lanes of token m
+  const float r = rsqrt_ieee(ss / (float)HD + a.eps);
+  const bf16* wn = head < NH ? qn : kn;
+  float n[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) n[q] = rbf(rbf(x[q] * r) * bf2f(wn[j + 32 * q]));
+  if (!act || !pok) return;
+  // rotate-half pairs: (j, j+64) and (j+32, j+96)
+  const size_t cb = (size_t)p * HD;
+  float o4[4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int d = j + 32 * q;                  // d < 64, partner d + 64
+    const float c1 = bf2f(a.cos_t[cb + d]), c2 = bf2f(a.cos_t[cb + d + 64]);
+    const float s1 = bf2f(a.sin_t[cb + d]), s2 = bf2f(a.sin_t[cb + d + 64]);
+    o4[q] = rbf(rbf(n[q] * c1) + rbf(-n[q + 2] * s1));
+    o4[q + 2] = rbf(rbf(n[q + 2] * c2) + rbf(n[q] * s2));
+  }
+  if (head < NH) {
+    const rsrc_t qr = make_rsrc(a.qbuf, (unsigned)((size_t)M * NH * HD * 2));
+    const size_t base = ((size_t)m * NH + head) * HD;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) stc_b16(qr, (unsigned)((base + j + 32 * q) * 2), f2bf(o4[q]));
+  } else {
+    const rsrc_t kr = make_rsrc(kc, (unsigned)((size_t)M * NKV * a.cap * HD * 2));
+    const size_t base = (((size_t)m * NKV + (head - NH)) * a.cap + p) * HD;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) stc_b16(kr, (unsigned)((base + j + 32 * q) * 2), f2bf(o4[q]));
+  }
+}
+
+__device__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp) {
+  // 64 residual columns grp*64 .. : h = bf16(h + bf16(sum)); ss[grp][m] = sum_c h^2
+  const int M = a.M;
+  const int t = threadIdx.x;
+  const int m = t >> 5, c2 = (t & 31) * 2;   // two columns per thread
+  const rsrc_t hr = make_rsrc(a.h, (unsigned)((size_t)M * a.H * 2));
+  float q = 0.f;
+  if (m < M) {
+    const unsigned off = (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2;
+    const unsigned hv2 = ldc_u32(hr, off);
+    const float h0 = rbf(lo_bf(hv2) + rbf(res[c2][m]));
+    const float h1 = rbf(hi_bf(hv2) + rbf(res[c2 + 1][m]));
+    stc_u32(hr, off, (unsigned)f2bf(h0) | ((unsigned)f2bf(h1) << 16));
+    q = h0 * h0 + h1 * h1;
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+  if (m < M && (t & 31) == 0) {
+    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
+    stc_f32(ssr, (unsigned)(grp * MAXM + m) * 4, q);
+  }
+}
+
+__device__ void epi_silu(const Args& a, float (*res)[MAXM + 1], int grp) {
+  // rows 0..15: gate features grp*16.., rows 16..31: the matching up rows
+  const int M = a.M;
+  const int t = threadIdx.x;
+  if (t >= 16 * MAXM) return;
+  const int m = t >> 4, f = t & 15;
+  if (m >= M) return;
+  const float g = rbf(res[f][m]);
+  const float u = rbf(res[16 + f][m]);
+  const float s = rbf(g / (1.0f + expf(-g)));
+  const rsrc_t mr = make_rsrc(a.mbuf, (unsigned)((size_t)M * a.I * 2));
+  stc_b16(mr, (unsigned)((size_t)m * a.I + grp * 16 + f) * 2, f2bf(s * u));
+}
+
+__device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+
+__device__ void epi_logits(const Args& a, Shared& sh, float (*res)[MAXM + 1], int grp) {
+  // 32 vocab rows grp*32 ..; logits out + the workgroup's running argmax per token
+  const int M = a.M;
+  const int t = threadIdx.x;
+  const int m = t >> 5, v = t & 31;
+  float val = -INFINITY;
+  int idx = 0x7fffffff;
+  if (m < M) {
+    const bf16 b = f2bf(res[v][m]);
+    const int col = grp * 32 + v;
+    a.logits[(size_t)m * a.V + col] = b;
+    val = bf2f(b);
+    idx = col;
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(val, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (am_better(ov, oi, val, idx)) { val = ov; idx = oi; }
+  }
+  if (m < M && v == 0 && am_better(val, idx, sh.bestv[m], sh.besti[m])) {
+    sh.bestv[m] = val;
+    sh.besti[m] = idx;
+  }
+}
+
+// Reduce the waves' tiles of one row group, finish the group (directly, or through partials
+// when it is shared with other workgroups) and run the epilogue.
+template <int NR, int EPI>
+__device__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
+                            f32x4 (&acc)[NR]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int M = a.M;
+  GemvLds<NR> L(sh);
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L.red[wave][t][lane * 4 + i] = acc[t][i];
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes done (vmcnt untouched)
+  __builtin_amdgcn_s_barrier();
+  // res[row][m], row = t*16 + (lane/16)*4 + i of the D layout, m = lane % 16
+  for (int e = threadIdx.x; e < NR * 256; e += NTHR) {
+    const int t = e >> 8, ln = (e >> 2) & 63, i = e & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) s += L.red[w][t][ln * 4 + i];
+    L.res[t * 16 + (ln >> 4) * 4 + i][ln & 15] = s;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  const int first = wg_of_step(g, grp * g.nk);
+  const int last = wg_of_step(g, (grp + 1) * g.nk - 1);
+  bool finish = true;
+  if (first != last) {
+    // partial: slot 0 = the group holding this workgroup's first step, slot 1 = its last
+    const int rows = NR * 16;
+    const unsigned slot_floats = (unsigned)(rows * MAXM);
+    const rsrc_t pr = make_rsrc(a.ws + a.off_part, (unsigned)(gridDim.x * 2 * slot_floats * 4));
+    const int myslot = (grp == g.s0 / g.nk) ? 0 : 1;
+    for (int e = threadIdx.x; e < rows * M; e += NTHR) {
+      const int row = e / M, m = e - (e / M) * M;
+      stc_f32(pr, ((blockIdx.x * 2 + myslot) * slot_floats + row * MAXM + m) * 4,
+              L.res[row][m]);
+    }
+    // contributors: the workgroups first..last whose step range is not empty
+    int ncontrib = 0;
+    for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
+    finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
+    if (finish) {
+      for (int e = threadIdx.x; e < rows * M; e += NTHR) {
+        const int row = e / M, m = e - (e / M) * M;
+        float s = 0.f;
+        for (int c = first; c <= last; ++c) {
+          const int cs0 = step0_of(g, c);
+          if (step0_of(g, c + 1) == cs0) continue;
+          const int slot = (grp == cs0 / g.nk) ? 0 : 1;
+          s += ldc_f32(pr, ((c * 2 + slot) * slot_floats + row * MAXM + m) * 4);
+        }
+        L.res[row][m] = s;
+      }
+      __syncthreads();
+    }
+  }
+  if (finish) {
+    if (EPI == EPI_QKV) epi_qkv(a, L.res, layer, grp);
+    else if (EPI == EPI_RES) epi_res(a, L.res, grp);
+    else if (EPI == EPI_SILU) epi_silu(a, L.res, grp);
+    else epi_logits(a, sh, L.res, grp);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+}
+
+// Consume this workgroup's steps of a GEMV phase. On entry cur/nxt hold (in flight) the wave's
+// batches 0 and 1. Returns with nothing in flight.
+template <int NR, int EPI>
+__device__ void gemv_phase(const Args& a, Shared& sh, const Geo& g, int layer,
+                           u32x4 (&cur)[BATCH], u32x4 (&nxt)[BATCH]) {
+  constexpr int U = BATCH / NR;   // steps per batch
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int M = a.M;
+  const int nmine = g.s1 - g.s0 > wave ? (g.s1 - g.s0 - wave + NWAVE - 1) / NWAVE : 0;
+  const int seg0 = g.s1 > g.s0 ? g.s0 / g.nk : 0;
+  const int nseg = g.s1 > g.s0 ? (g.s1 - 1) / g.nk - seg0 + 1 : 0;
+  const unsigned char* xb = GemvLds<NR>(sh).x;
+  const int xrow = min(lane & 15, M - 1) * sh.xrs + (lane >> 4) * 16;
+  const int ksf = sh.xksf;
+  f32x4 acc[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int flushed = 0;
+  for (int j = 0;; ++j) {
+    int target = nseg, s = 0, grp = 0;
+    if (j < nmine) {
+      s = g.s0 + wave + NWAVE * j;
+      grp = s / g.nk;
+      target = grp - seg0;
+    }
+    while (flushed < target) {
+      flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, acc);
+      ++flushed;
+    }
+    if (j >= nmine) break;
+    int w = s - grp * g.nk - ksf;
+    if (w < 0) w += g.nk;
+    const u32x4 xv = *(const u32x4*)(xb + xrow + w * 64);
+#pragma unroll
+    for (int t = 0; t < NR; ++t) acc[t] = mfma16x16x32(cur[t], xv, acc[t]);
+    if ((j + 1) % U == 0) {
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) cur[b] = nxt[b];
+      issue_batch<NR>(g, j + 1 + U, nxt);
+    } else {
+#pragma unroll
+      for (int b = 0; b + NR < BATCH; ++b) cur[b] = cur[b + NR];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// attention: units (row b, kv head, chunk of C keys); see attn.hip for the MFMA formulation.
+__device__ void attention_phase(const Args& a, Shared& sh, int layer) {
+  const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV, C = a.chunk;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int64_t* lp = a.layers + (size_t)layer * NFIELD;
+  const bf16* kc = (const bf16*)lp[F_KC];
+  const bf16* vc = (const bf16*)lp[F_VC];
+  const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int b = 0; b < M; ++b) {
+      sh.units[b] = acc;
+      const int64_t p = a.pos[b];
+      const int L = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
+      acc += NKV * ((L + C - 1) / C);
+    }
+    sh.units[M] = acc;
+  }
+  __syncthreads();
+  const int U = sh.units[M];
+  const int u0 = (int)((long long)U * blockIdx.x / gridDim.x);
+  const int u1 = (int)((long long)U * (blockIdx.x + 1) / gridDim.x);
+  const size_t kvrow = (size_t)HD;
+  const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
+  const rsrc_t kr = make_rsrc(kc, kvbytes), vr = make_rsrc(vc, kvbytes);
+  const rsrc_t qr = make_rsrc(a.qbuf, (unsigned)((size_t)M * NH * HD * 2));
+  const rsrc_t orr = make_rsrc(a.attn, (unsigned)((size_t)M * NH * HD * 2));
+  const int maxch = (a.cap + C - 1) / C;
+  const unsigned wsrow = HD + 2;
+  const rsrc_t pr = make_rsrc(a.ws + a.off_att, (unsigned)((size_t)MAXM * NKV * maxch * G * wsrow * 4));
+  for (int u = u0; u < u1; ++u) {
+    int b = 0;
+    while (b + 1 < M && sh.units[b + 1] <= u) ++b;
+    const int64_t p0 = a.pos[b];
+    const int L = (int)min<int64_t>(p0 + 1, (int64_t)a.cap);
+    const int nch = (L + C - 1) / C;
+    const int r = u - sh.units[b];
+    const int kvh = r / nch, c = r - (r / nch) * nch;
+    const int start = c * C, end = min(start + C, L);
+    const int bk = b * NKV + kvh;
+    const size_t kvbase = (size_t)bk * a.cap * kvrow;
+    // Q^T operand (rows = the G query heads of this kv head; rows >= G zero)
+    u32x4 qreg[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      qreg[kb] = l16 < G ? ldc_b128(qr, (unsigned)((((size_t)b * NH + kvh * G + l16) * HD + kb * 32 + g4 * 8) * 2))
+                         : u32x4{0u, 0u, 0u, 0u};
+    f32x4 acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    bf16(*vs)[HD + 8] = sh.u.a.v[wave];
+    const int nblk = (end - start + 31) >> 5;
+    for (int bi = wave; bi < nblk; bi += NWAVE) {
+      const int j0 = start + bi * 32;
+      // the block holding the newest key (written this launch) is read through sc1
+      const bool fresh = j0 + 31 >= (int)p0;
+      u32x4 kreg[2][4];
+      u32x4 vreg[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        int key = j0 + t * 16 + l16;
+        key = key < a.cap ? key : a.cap - 1;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const size_t off = kvbase + (size_t)key * kvrow + kb * 32 + g4 * 8;
+          kreg[t][kb] = fresh ? ldc_b128(kr, (unsigned)(off * 2)) : ld16(kc + off);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int cc = it * 64 + lane;
+        int key = j0 + (cc >> 4);
+        key = key < a.cap ? key : a.cap - 1;
+        const size_t off = kvbase + (size_t)key * kvrow + (cc & 15) * 8;
+        vreg[it] = fresh ? ldc_b128(vr, (unsigned)(off * 2)) : ld16(vc + off);
+      }
+      f32x4 sc[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) d = mfma16x16x32(kreg[t][kb], qreg[kb], d);
+        sc[t] = d;
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int cc = it * 64 + lane;
+        *(u32x4*)&vs[cc >> 4][(cc & 15) * 8] = vreg[it];
+      }
+      float sv[8];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = j0 + t * 16 + g4 * 4 + i;
+          const float v = key < end ? sc[t][i] * scale_log2 : -INFINITY;
+          sv[t * 4 + i] = v;
+          mloc = fmaxf(mloc, v);
+        }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run, mloc);
+      const float msafe = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run - msafe);
+      float psum = 0.f;
+      unsigned pk[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float pa = exp2f(sv[2 * jj] - msafe);
+        const float pb = exp2f(sv[2 * jj + 1] - msafe);
+        psum += pa + pb;
+        pk[jj] = (unsigned)f2bf(pa) | ((unsigned)f2bf(pb) << 16);
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int d = dt * 16 + l16;
+        unsigned av[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int ka = (jj < 2) ? (g4 * 4 + 2 * jj) : (16 + g4 * 4 + 2 * (jj - 2));
+          av[jj] = (unsigned)vs[ka][d] | ((unsigned)vs[ka + 1][d] << 16);
+        }
+        acc[dt] = mfma16x16x32(u32x4{av[0], av[1], av[2], av[3]}, pB, acc[dt]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // merge the waves (rows < G)
+    __syncthreads();
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sh.u.a.mrg[wave][l16][dt * 16 + g4 * 4 + i] = acc[dt][i];
+    if (g4 == 0) {
+      sh.ms[wave][l16] = m_run;
+      sh.ls[wave][l16] = l_run;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * HD; e += NTHR) {
+      const int row = e / HD, d = e % HD;
+      float Mx = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w) Mx = fmaxf(Mx, sh.ms[w][row]);
+      const float Ms = Mx == -INFINITY ? 0.f : Mx;
+      float o = 0.f, l = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w) {
+        const float f = exp2f(sh.ms[w][row] - Ms);
+        o += sh.u.a.mrg[w][row][d] * f;
+        l += sh.ls[w][row] * f;
+      }
+      const unsigned oidx = (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2;
+      if (nch == 1) {
+        stc_b16(orr, oidx, f2bf(o / l));
+      } else {
+        const unsigned pb = (unsigned)((((size_t)bk * maxch + c) * G + row) * wsrow) * 4;
+        stc_f32(pr, pb + d * 4, o);
+        if (d == 0) {
+          stc_f32(pr, pb + HD * 4, Mx);
+          stc_f32(pr, pb + (HD + 1) * 4, l);
+        }
+      }
+    }
+    if (nch > 1 && arrive_last(a.ctr + C_ATT + bk, nch, &sh.flag)) {
+      for (int e = threadIdx.x; e < G * HD; e += NTHR) {
+        const int row = e / HD, d = e % HD;
+        const unsigned pb0 = (unsigned)((((size_t)bk * maxch) * G + row) * wsrow) * 4;
+        const unsigned cs = (unsigned)(G * wsrow) * 4;
+        float Mx = -INFINITY;
+        for (int q = 0; q < nch; ++q) Mx = fmaxf(Mx, ldc_f32(pr, pb0 + q * cs + HD * 4));
+        float o = 0.f, l = 0.f;
+        for (int q = 0; q < nch; ++q) {
+          const float f = exp2f(ldc_f32(pr, pb0 + q * cs + HD * 4) - Mx);
+          o += ldc_f32(pr, pb0 + q * cs + d * 4) * f;
+          l += ldc_f32(pr, pb0 + q * cs + (HD + 1) * 4) * f;
+        }
+        stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// embedding gather: workgroup q < H/64 copies columns q*64.. of every row, stores ss[q][m]
+__device__ void embed_phase(const Args& a, Shared& sh) {
+  const int M = a.M;
+  const int q = blockIdx.x;
+  if (q >= a.H / SSG) return;
+  const int t = threadIdx.x;
+  const int m = t >> 5, c2 = (t & 31) * 2;
+  float s = 0.f;
+  if (m < M) {
+    int64_t tk = a.tok[m];
+    if (tk < 0 || tk >= a.V) {
+      if (c2 == 0) atomicOr(a.err, E_TOKEN);
+      tk = 0;
+    }
+    const unsigned v2 = *(const unsigned*)(a.embed + (size_t)tk * a.H + q * SSG + c2);
+    const rsrc_t hr = make_rsrc(a.h, (unsigned)((size_t)M * a.H * 2));
+    stc_u32(hr, (unsigned)((size_t)m * a.H + q * SSG + c2) * 2, v2);
+    s = lo_bf(v2) * lo_bf(v2) + hi_bf(v2) * hi_bf(v2);
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (m < M && (t & 31) == 0) {
+    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
+    stc_f32(ssr, (unsigned)(q * MAXM + m) * 4, s);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// phase table
+enum { P_EMB = 0, P_QKV = 1, P_ATT = 2, P_O = 3, P_GU = 4, P_D = 5, P_LM = 6 };
+
+__device__ __forceinline__ int phase_kind(const Args& a, int p, int* layer) {
+  if (p == 0) { *layer = -1; return P_EMB; }
+  if (p == 1 + 5 * a.L) { *layer = -1; return P_LM; }
+  *layer = (p - 1) / 5;
+  return P_QKV + (p - 1) % 5;
+}
+
+__device__ __forceinline__ bool phase_geo(const Args& a, int p, Geo* g) {
+  int layer;
+  const int kind = phase_kind(a, p, &layer);
+  const int64_t* lp = layer >= 0 ? a.layers + (size_t)layer * NFIELD : nullptr;
+  switch (kind) {
+    case P_QKV: *g = make_geo((const bf16*)lp[F_WQKV], (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV); return true;
+    case P_O:   *g = make_geo((const bf16*)lp[F_WO], a.H, a.NH * HD, LNR_O); return true;
+    case P_GU:  *g = make_geo((const bf16*)lp[F_WGU], 2 * a.I, a.H, LNR_GU); return true;
+    case P_D:   *g = make_geo((const bf16*)lp[F_WD], a.H, a.I, LNR_D); return true;
+    case P_LM:  *g = make_geo(a.lm_t, a.V, a.H, LNR_LM); return true;
+    default: return false;
+  }
+}
+
+// One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, stage
+// the activation window, consume. The prefetch registers live only inside this call.
+template <int LNR, int EPI>
+__device__ void run_gemv(const Args& a, Shared& sh, const Geo& g, int layer, bool sync,
+                         unsigned epoch, int K, const bf16* src, const bf16* lnw) {
+  constexpr int NR = 1 << LNR;
+  u32x4 cur[BATCH], nxt[BATCH];
+  if (sync) bar_arrive(a, epoch);
+  issue_batch<NR>(g, 0, cur);
+  issue_batch<NR>(g, BATCH / NR, nxt);
+  if (sync) bar_wait(a, sh, epoch);
+  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw);
+  gemv_phase<NR, EPI>(a, sh, g, layer, cur, nxt);
+}
+
+__global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
+  extern __shared__ unsigned char smem_raw[];
+  Shared& sh = *(Shared*)smem_raw;
+  unsigned epoch = 0;
+  if (threadIdx.x < MAXM) {
+    sh.bestv[threadIdx.x] = -INFINITY;
+    sh.besti[threadIdx.x] = 0x7fffffff;
+  }
+  if (threadIdx.x == 0) sh.bail = 0;
+  __syncthreads();
+  for (int p = a.phase_begin; p < a.phase_end; ++p) {
+    int layer;
+    const int kind = phase_kind(a, p, &layer);
+    const int64_t* lp = layer >= 0 ? a.layers + (size_t)layer * NFIELD : nullptr;
+    const bool sync = p > a.phase_begin;
+    if (sync) ++epoch;
+    Geo g;
+    phase_geo(a, p, &g);
+    switch (kind) {
+      case P_QKV:
+        run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, layer, sync, epoch, a.H, a.h, (const bf16*)lp[F_LN1]);
+        break;
+      case P_O:
+        run_gemv<LNR_O, EPI_RES>(a, sh, g, layer, sync, epoch, a.NH * HD, a.attn, nullptr);
+        break;
+      case P_GU:
+        run_gemv<LNR_GU, EPI_SILU>(a, sh, g, layer, sync, epoch, a.H, a.h, (const bf16*)lp[F_LN2]);
+        break;
+      case P_D:
+        run_gemv<LNR_D, EPI_RES>(a, sh, g, layer, sync, epoch, a.I, a.mbuf, nullptr);
+        break;
+      case P_LM:
+        run_gemv<LNR_LM, EPI_LOGITS>(a, sh, g, layer, sync, epoch, a.H, a.h, a.fnorm);
+        break;
+      default:
+        if (sync) {
+          bar_arrive(a, epoch);
+          bar_wait(a, sh, epoch);
+        }
+        if (kind == P_EMB) embed_phase(a, sh);
+        else attention_phase(a, sh, layer);
+        break;
+    }
+    if (kind == P_LM) {
+      // argmax over the workgroups' candidates; the last workgroup writes tok, advances pos
+      const rsrc_t cr = make_rsrc(a.ws + a.off_am, (unsigned)(gridDim.x * MAXM * 2 * 4));
+      if (threadIdx.x < (unsigned)a.M) {
+        stc_f32(cr, (unsigned)((blockIdx.x * MAXM + threadIdx.x) * 2) * 4, sh.bestv[threadIdx.x]);
+        stc_u32(cr, (unsigned)((blockIdx.x * MAXM + threadIdx.x) * 2 + 1) * 4, (unsigned)sh.besti[threadIdx.x]);
+      }
+      if (arrive_last(a.ctr + C_AM, gridDim.x, &sh.flag)) {
+        if (threadIdx.x < 64) {
+          for (int m = 0; m < a.M; ++m) {
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int w = threadIdx.x; w < (int)gridDim.x; w += 64) {
+              const float v = ldc_f32(cr, (unsigned)((w * MAXM + m) * 2) * 4);
+              const int i = (int)ldc_u32(cr, (unsigned)((w * MAXM + m) * 2 + 1) * 4);
+              if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+              const float ov = __shfl_xor(bv, o, 64);
+              const int oi = __shfl_xor(bi, o, 64);
+              if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if (threadIdx.x == 0) {
+              a.tok[m] = bi;
+              a.pos[m] += 1;
+            }
+          }
+        }
+      }
+    }
+  }
+  // exit: the last workgroup out resets the barrier counters for the next launch
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(a.ctr + C_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (int)gridDim.x - 1) {
+      __hip_atomic_store(a.ctr + C_BAR, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int x = 0; x < 8; ++x)
+        __hip_atomic_store(a.ctr + C_BAR + 64 * (1 + x), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.ctr + C_EXIT, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// weight re-layout into MFMA tile order. Block (group gi, k-step ks, tile t) holds rows
+// src_row(gi, t, r), r = 0..15, columns ks*32 .. +32, lane l's 16 bytes = row l%16, k (l/16)*8.
+// gate/up (gu_I > 0, NR = 2): tile 0 = gate rows gi*16.., tile 1 = up rows gu_I + gi*16...
+__global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst, int N, int K,
+                                   int lnr, int gu_I) {
+  const size_t nblocks = (size_t)(N >> 4) * (K >> 5);
+  const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nblocks) return;
+  const int lane = threadIdx.x & 63;
+  const int nk = K >> 5;
+  const int NR = 1 << lnr;
+  const size_t step = blk >> lnr;
+  const int t = (int)(blk & (NR - 1));
+  const int gi = (int)(step / nk), ks = (int)(step % nk);
+  const int r = lane & 15;
+  int row;
+  if (gu_I > 0) row = (t == 0 ? 0 : gu_I) + gi * 16 + r;
+  else row = ((gi << lnr) + t) * 16 + r;
+  const u32x4 v = *(const u32x4*)(src + (size_t)row * K + ks * 32 + (lane >> 4) * 8);
+  *(u32x4*)(dst + (blk << 9) + lane * 8) = v;
+}
+
+}  // namespace st
+}  // namespace dd
+
+// ------------------------------------------------------------------------------------------
+// C ABI
+#include "api.h"
+
+using namespace dd;
+using namespace dd::st;
+
+static int step_grid(int* G_out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return (int)hipErrorInvalidDevice;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return (int)hipErrorInvalidDevice;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)decode_step_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(Shared)) !=
+        hipSuccess)
+      return (int)hipErrorInvalidConfiguration;
+    attr_set = true;
+  }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_step_kernel, NTHR, sizeof(Shared)) !=
+      hipSuccess || occ < 1)
+    return (int)hipErrorInvalidConfiguration;
+  *G_out = cus & ~7;   // barrier groups workgroups by XCD (8 per device)
+  return 0;
+}
+
+struct WsLayout { size_t ss, part, att, am, total; };
+
+static WsLayout ws_layout(int G, int NKV, int G_heads, int cap, int chunk) {
+  WsLayout w;
+  w.ss = 0;
+  w.part = 1024;                                            // ss: [H/64 <= 64][16]
+  w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // 2 slots of <= 128 rows x 16
+  const size_t maxch = (size_t)(cap + chunk - 1) / chunk;
+  w.am = w.att + (size_t)MAXM * NKV * maxch * G_heads * (HD + 2);
+  w.total = w.am + (size_t)G * MAXM * 2;
+  return w;
+}
+
+DD_API int dd_step_grid(void) {
+  int G = 0;
+  return step_grid(&G) == 0 ? G : -1;
+}
+
+DD_API int dd_step_counters(void) { return C_TOTAL; }
+
+DD_API size_t dd_step_ws_bytes(int NH, int NKV, int cap, int chunk) {
+  int G = 0;
+  if (step_grid(&G) != 0 || NKV < 1 || NH < NKV || cap < 1 || chunk < 32) return 0;
+  return ws_layout(G, NKV, NH / NKV, cap, chunk).total * sizeof(float);
+}
+
+DD_API size_t dd_tiled_bytes(int N, int K) { return (size_t)N * K * 2; }
+
+DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
+                          hipStream_t stream) {
+  DD_REQUIRE(src && dst && K % 32 == 0 && (nr == 1 || nr == 2 || nr == 4 || nr == 8));
+  const int lnr = nr == 1 ? 0 : nr == 2 ? 1 : nr == 4 ? 2 : 3;
+  DD_REQUIRE(N % (16 * nr) == 0);
+  DD_REQUIRE(gate_up_I == 0 || (nr == 2 && N == 2 * gate_up_I));
+  DD_REQUIRE(aligned16(src) && aligned16(dst));
+  const size_t nblocks = (size_t)(N / 16) * (K / 32);
+  hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((nblocks + 3) / 4)), dim3(256), 0, stream,
+                     (const bf16*)src, (bf16*)dst, N, K, lnr, gate_up_I);
+  return launch_status();
+}
+
+DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,
+                          const void* final_norm, const void* cos_t, const void* sin_t,
+                          int rope_rows, int64_t* tok, int64_t* pos, void* h, void* qbuf,
+                          void* attn, void* mbuf, void* logits, void* ws, int* counters, int* err,
+                          int M, int H, int NH, int NKV, int I, int V, int cap, float eps,
+                          int chunk, int phase_begin, int phase_end, hipStream_t stream) {
+  DD_REQUIRE(layer_table && embed && lm_tiled && final_norm && cos_t && sin_t && tok && pos);
+  DD_REQUIRE(h && qbuf && attn && mbuf && logits && ws && counters && err);
+  DD_REQUIRE(M >= 1 && M <= MAXM && L >= 1 && NKV >= 1 && NH % NKV == 0 && NH / NKV <= 16);
+  DD_REQUIRE(MAXM * NKV <= C_AM - C_ATT);   // one combine counter per (row, kv head)
+  // geometry the phases assume (Qwen3 family with head_dim 128)
+  DD_REQUIRE(H % SSG == 0 && H / SSG <= 64 && H % 32 == 0 && I % 32 == 0 && I % 16 == 0);
+  DD_REQUIRE(V % 32 == 0 && ((NH + 2 * NKV) * HD) % 128 == 0 && H % 64 == 0);
+  DD_REQUIRE(chunk >= 32 && chunk % 32 == 0 && cap >= 1 && rope_rows >= 1);
+  DD_REQUIRE(phase_begin >= 0 && phase_begin < phase_end && phase_end <= 2 + 5 * L);
+  int G = 0;
+  const int e = step_grid(&G);
+  if (e != 0) return e;
+  // the staged activation window of every GEMV phase must fit the LDS x buffer
+  {
+    const int K_of[4] = {H, NH * HD, H, I};
+    const int rows_of[4] = {(NH + 2 * NKV) * HD, H, 2 * I, H};
+    const int lnr_of[4] = {LNR_QKV, LNR_O, LNR_GU, LNR_D};
+    for (int q = 0; q < 5; ++q) {
+      const int K = q < 4 ? K_of[q] : H;
+      const int rows = q < 4 ? rows_of[q] : V;
+      const int lnr = q < 4 ? lnr_of[q] : LNR_LM;
+      const long long S = (long long)(rows >> (4 + lnr)) * (K / 32);
+      const long long per = (S + G - 1) / G;
+      const long long nw = per < K / 32 ? per : K / 32;
+      DD_REQUIRE((nw * 64 + 16) * M <= (long long)x_capacity(1 << lnr));
+      DD_REQUIRE((rows >> (4 + lnr)) <= 8192);
+    }
+  }
+  const WsLayout w = ws_layout(G, NKV, NH / NKV, cap, chunk);
+  Args a;
+  a.layers = layer_table;
+  a.embed = (const bf16*)embed;
+  a.lm_t = (const bf16*)lm_tiled;
+  a.fnorm = (const bf16*)final_norm;
+  a.cos_t = (const bf16*)cos_t;
+  a.sin_t = (const bf16*)sin_t;
+  a.tok = tok;
+  a.pos = pos;
+  a.h = (bf16*)h;
+  a.qbuf = (bf16*)qbuf;
+  a.attn = (bf16*)attn;
+  a.mbuf = (bf16*)mbuf;
+  a.logits = (bf16*)logits;
+  a.ws = (float*)ws;
+  a.ctr = counters;
+  a.err = err;
+  a.L = L; a.M = M; a.H = H; a.NH = NH; a.NKV = NKV; a.I = I; a.V = V;
+  a.cap = cap; a.rope_rows = rope_rows; a.chunk = chunk; a.eps = eps;
+  a.phase_begin = phase_begin;
+  a.phase_end = phase_end;
+  a.off_ss = (unsigned)w.ss;
+  a.off_part = (unsigned)w.part;
+  a.off_att = (unsigned)w.att;
+  a.off_am = (unsigned)w.am;
+  a.ws_floats = (unsigned)w.total;
+  hipLaunchKernelGGL(decode_step_kernel, dim3(G), dim3(NTHR), sizeof(Shared), stream, a);
+  return launch_status();
+}

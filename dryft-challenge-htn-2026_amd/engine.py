@@ -23,6 +23,7 @@ import os
 import torch
 
 from .hipops import HipOps, TorchOps
+from .step import FusedStep
 
 CAP_GRAN = 128        # engine.py:24
 MAX_STATES = 6        # engine.py:94
@@ -102,7 +103,9 @@ class Engine:
         self._dbg = None
         self.pool = torch.cuda.graph_pool_handle()
         self.ops = None
+        self.step = None
         self.ops = self._select_ops(selftest)
+        self.step = self._select_step(selftest)
 
     @classmethod
     def from_state_dict(cls, cfg, weights, **kw):
@@ -171,17 +174,37 @@ class Engine:
             ops = _Mixed(ops, TorchOps(self), off)
         return ops
 
-    def _selftest(self, candidate):
+    def _select_step(self, selftest):
+        """The one-launch decode step (FusedStep) for states it takes (B <= 16, W == 1), checked
+        like the ops: 3 teacher-forced steps against torch ops. ENGINE_STEP=0 turns it off;
+        a failed check leaves the per-op HipOps graph in charge (also HIP)."""
+        if os.environ.get("ENGINE_STEP") == "0" or isinstance(self.ops, (TorchOps, _Mixed)):
+            return None
+        try:
+            step = FusedStep(self)
+        except RuntimeError as ex:
+            print(f"[engine] fused decode step unavailable: {ex}")
+            return None
+        if selftest:
+            diff = self._selftest(self.ops, step)
+            print(f"[engine] fused decode step selftest max logit diff {diff:.4f}")
+            if not diff <= 0.5:
+                print("[engine] fused decode step failed its self-test; using per-op kernels")
+                return None
+        return step
+
+    def _selftest(self, candidate, step=None):
         """engine.py:629-680 contract: prefill B=2, S=96, then 3 teacher-forced decode steps with
-        the candidate ops vs torch ops on the same weights; returns the max logit difference."""
+        the candidate ops (and decode step) vs torch ops on the same weights; returns the max
+        logit difference."""
         torch.manual_seed(0)
         B, S, n = 2, 96, 4
         high = min(5000, self.embed.shape[0])
         ids = torch.randint(min(100, high - 1), high, (B, S), device=self.dev)
 
-        def run(ops, forced=None):
-            saved = self.ops
-            self.ops = ops
+        def run(ops, step, forced=None):
+            saved = self.ops, self.step
+            self.ops, self.step = ops, step
             try:
                 st = self._new_state(B, 128)
                 self._dbg, toks = [], []
@@ -195,10 +218,10 @@ class Engine:
                 return self._dbg, toks
             finally:
                 self._dbg = None
-                self.ops = saved
+                self.ops, self.step = saved
 
-        ref, toks = run(TorchOps(self))
-        got, _ = run(candidate, toks)
+        ref, toks = run(TorchOps(self), None)
+        got, _ = run(candidate, step, toks)
         diffs = [(r - g).abs().max().item() for r, g in zip(ref, got)]
         return max(diffs) if all(math.isfinite(d) for d in diffs) else float("inf")
 
@@ -215,6 +238,9 @@ class Engine:
         st.pos = torch.zeros(B, dtype=torch.long, device=self.dev)
         st.graph = None
         st.hcap = 0
+        st.fused = None
+        if self.step is not None and FusedStep.supports(B, W):
+            self.step.bind(st)
         return st
 
     def _state(self, B, cap, W=1, graph=True):
@@ -298,7 +324,14 @@ class Engine:
         return logits
 
     def _decode_body(self, st):
-        """engine.py:538-540: tok <- argmax(forward(tok, pos)); pos += 1 (fused in one kernel)."""
+        """engine.py:538-540: tok <- argmax(forward(tok, pos)); pos += 1. States bound to the
+        fused step run it as one launch; others run the per-op kernels (argmax and pos += 1
+        fused in one kernel)."""
+        if st.fused is not None:
+            logits = self.step.run(st)
+            if self._dbg is not None:
+                self._dbg.append(logits.float().cpu())
+            return
         logits = self._forward(st, st.tok, st.W, st.pos)
         if hasattr(self.ops, "argmax_"):
             self.ops.argmax_(logits, st.tok, st.pos)
@@ -374,6 +407,10 @@ class Engine:
 
     def error_flags(self):
         """Device error word of the kernels (1: token id out of range, 2: position outside the
-        cache / rope table). Synchronises."""
+        cache / rope table, 4: a grid barrier of the fused step timed out). Synchronises."""
         ops = self.ops.f if isinstance(self.ops, _Mixed) else self.ops
-        return int(ops.err.item()) if hasattr(ops, "err") else 0
+        flags = int(ops.err.item()) if hasattr(ops, "err") else 0
+        for st in self.states.values():
+            if st.fused is not None:
+                flags |= int(st.fused.err.item())
+        return flags

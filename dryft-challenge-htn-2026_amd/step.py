@@ -1,0 +1,113 @@
+"""``FusedStep``: the whole greedy decode step as ONE persistent kernel launch (dd_decode_step).
+
+The reference runs a decode step as a CUDA graph of ~10 kernels per layer
+(``Engine._capture``, engine/engine.py:380-396, replaying ``_decode_body`` engine.py:538-540
+over ``_forward`` engine.py:459-503). On MI355X the per-kernel launch gaps and the tail of every
+small GEMV cost more than the weight stream itself at decode batch sizes, so this path runs the
+step's phases (embedding; per layer QKV+norm+RoPE+KV write, attention, O+residual,
+gate/up+SiLU, down+residual; lm_head+argmax) inside one launch of one workgroup per CU, with
+grid barriers between phases and every weight matrix streamed from a copy re-laid out once in
+MFMA tile order (``dd_tile_weight``).
+
+Same arithmetic and rounding points as ``HipOps`` / the reference ``_TorchOps``; it takes
+``B <= 16`` rows and one token per row (``W == 1``). The engine uses it for those states and
+the per-op ``HipOps`` graph otherwise (both are HIP; there is no CPU path).
+"""
+import ctypes
+
+import torch
+
+from ._lib import check, lib
+
+MAXM = 16
+HD = 128
+NFIELD = 16
+# tiles per row group (the kernel's compile-time layout): wqkv, wo, wgu, wd, lm_head
+NR_QKV, NR_O, NR_GU, NR_D, NR_LM = 8, 4, 2, 4, 2
+CHUNK = 256           # keys per attention split
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class FusedStep:
+    """Tiled weights of one engine plus per-state buffers for ``dd_decode_step``."""
+
+    def __init__(self, e):
+        self.e = e
+        self.L = lib()
+        self.grid = self.L.dd_step_grid()
+        if self.grid <= 0:
+            raise RuntimeError("dd_step_grid: the persistent decode kernel cannot be resident")
+        if e.hd != HD:
+            raise RuntimeError(f"fused decode step needs head_dim {HD}, got {e.hd}")
+        self.H = e.embed.shape[1]
+        self.V = e.embed.shape[0] if e.lm_head is e.embed else e.lm_head.shape[0]
+        self.I = e.layers[0].wd.shape[1]
+        with torch.no_grad():
+            for l in e.layers:
+                l.wqkv_t = self._tile(l.wqkv, NR_QKV)
+                l.wo_t = self._tile(l.wo, NR_O)
+                l.wgu_t = self._tile(l.wgu, NR_GU, gate_up_I=self.I)
+                l.wd_t = self._tile(l.wd, NR_D)
+            self.lm_t = self._tile(e.lm_head, NR_LM)
+        torch.cuda.synchronize(e.dev)
+
+    def _tile(self, w, nr, gate_up_I=0):
+        N, K = w.shape
+        out = torch.empty(self.L.dd_tiled_bytes(N, K) // 2, dtype=torch.bfloat16, device=w.device)
+        check(self.L.dd_tile_weight(w.data_ptr(), out.data_ptr(), N, K, nr, gate_up_I,
+                                    _stream(w.device)), "dd_tile_weight")
+        return out
+
+    @staticmethod
+    def supports(B, W):
+        return W == 1 and 1 <= B <= MAXM
+
+    def bind(self, st):
+        """Allocate the step's buffers for a state and build its layer table (the KV cache
+        tensors of the state are baked in: one table per state)."""
+        e, dev = self.e, self.e.dev
+        B, H, I, V = st.B, self.H, self.I, self.V
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        f = _State()
+        f.h = torch.empty(B, H, **bf)
+        f.qbuf = torch.empty(B, e.nh * HD, **bf)
+        f.attn = torch.empty(B, e.nh * HD, **bf)
+        f.mbuf = torch.empty(B, I, **bf)
+        f.logits = torch.empty(B, V, **bf)
+        ws = self.L.dd_step_ws_bytes(e.nh, e.nkv, st.cap, CHUNK)
+        if ws == 0:
+            raise RuntimeError("dd_step_ws_bytes rejected the shape")
+        f.ws = torch.empty(ws // 4, dtype=torch.float32, device=dev)
+        f.counters = torch.zeros(self.L.dd_step_counters(), dtype=torch.int32, device=dev)
+        f.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        table = torch.zeros(e.L, NFIELD, dtype=torch.int64)
+        for i, l in enumerate(e.layers):
+            table[i, :10] = torch.tensor([
+                l.wqkv_t.data_ptr(), l.wo_t.data_ptr(), l.wgu_t.data_ptr(), l.wd_t.data_ptr(),
+                l.ln1.data_ptr(), l.ln2.data_ptr(), l.qn.data_ptr(), l.kn.data_ptr(),
+                st.kc[i].data_ptr(), st.vc[i].data_ptr()], dtype=torch.int64)
+        f.table = table.to(dev)
+        st.fused = f
+
+    def run(self, st, phase_begin=0, phase_end=None):
+        """One decode step: st.tok <- argmax(logits(st.tok at st.pos)), st.pos += 1; the
+        logits stay in st.fused.logits."""
+        e, f = self.e, st.fused
+        if phase_end is None:
+            phase_end = 2 + 5 * e.L
+        check(self.L.dd_decode_step(
+            f.table.data_ptr(), e.L, e.embed.data_ptr(), self.lm_t.data_ptr(), e.norm.data_ptr(),
+            e.cos.data_ptr(), e.sin.data_ptr(), e.cos.shape[0], st.tok.data_ptr(),
+            st.pos.data_ptr(), f.h.data_ptr(), f.qbuf.data_ptr(), f.attn.data_ptr(),
+            f.mbuf.data_ptr(), f.logits.data_ptr(), f.ws.data_ptr(), f.counters.data_ptr(),
+            f.err.data_ptr(), st.B, self.H, e.nh, e.nkv, self.I, self.V, st.cap,
+            ctypes.c_float(e.eps), CHUNK, phase_begin, phase_end, _stream(e.dev)),
+            "dd_decode_step")
+        return f.logits
+
+
+class _State:
+    pass

@@ -118,6 +118,46 @@ int dd_argmax(const void* logits, int M, int V, int64_t* tok, int64_t* pos, int 
               int* counters, hipStream_t stream);
 size_t dd_argmax_ws_bytes(int M, int V);
 
+/* ---- whole decode step in one persistent launch ------------------------------------------
+ * One launch runs Engine._decode_body for M <= 16 rows, one token each: embedding, every layer
+ * (QKV + q/k RMSNorm + RoPE + K/V write, attention, O + residual, gate/up + SiLU, down +
+ * residual), final RMSNorm, lm_head, argmax, pos += 1. Replaces the body of
+ * Engine._forward(pos=...) + _decode_body (engine.py:459-503, 538-540) that the reference
+ * captures into one CUDA graph (engine.py:380-396) and replays per token (engine.py:722).
+ *
+ * The launch has dd_step_grid() workgroups that must all be resident at once (one per CU, the
+ * device to itself); they meet at grid barriers between phases, each wait bounded by a 200 ms
+ * timeout that sets err flag 4 instead of hanging.
+ *
+ * Weights are streamed from a tiled copy made once by dd_tile_weight (the natural row-major
+ * matrices stay the interface): block (row group g, k-step s, tile t) = the 16 x 32 bf16
+ * MFMA A-operand of rows (g*nr + t)*16 .. +16, columns s*32 .. +32, 1 KB in lane order
+ * (lane l: row l%16, columns (l/16)*8 .. +8). gate_up_I > 0 (nr = 2) interleaves gate and up:
+ * tile 0 = gate rows g*16.., tile 1 = up rows gate_up_I + g*16... nr per matrix: wqkv 8,
+ * wo 4, wgu 2 (gate_up_I = I), wd 4, lm_head 2. dst holds dd_tiled_bytes(N, K). */
+int dd_step_grid(void);
+int dd_step_counters(void);
+size_t dd_step_ws_bytes(int NH, int NKV, int cap, int chunk);
+size_t dd_tiled_bytes(int N, int K);
+int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
+                   hipStream_t stream);
+
+/* layer_table: [L][16] int64 device pointers per layer: 0 wqkv (tiled), 1 wo (tiled),
+ * 2 wgu (tiled), 3 wd (tiled), 4 input_layernorm, 5 post_attention_layernorm, 6 q_norm,
+ * 7 k_norm, 8 K cache, 9 V cache ([M, NKV, cap, 128] each); 10..15 unused.
+ * tok/pos: [M] int64 (in: this step's tokens and positions; out: the argmax tokens, pos + 1).
+ * Buffers: h [M, H], qbuf [M, NH, 128], attn [M, NH*128], mbuf [M, I], logits [M, V] (bf16,
+ * logits hold the step's lm_head output afterwards); ws dd_step_ws_bytes; counters
+ * dd_step_counters() zeroed ints. chunk: keys per attention split (multiple of 32).
+ * phase_begin/phase_end select a sub-range of the 2 + 5L phases (0 embedding, 1 + 5l + {0 QKV,
+ * 1 attention, 2 O, 3 gate/up, 4 down}, 1 + 5L lm_head/argmax); a full step is 0 .. 2 + 5L. */
+int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,
+                   const void* final_norm, const void* cos_t, const void* sin_t, int rope_rows,
+                   int64_t* tok, int64_t* pos, void* h, void* qbuf, void* attn, void* mbuf,
+                   void* logits, void* ws, int* counters, int* err, int M, int H, int NH, int NKV,
+                   int I, int V, int cap, float eps, int chunk, int phase_begin, int phase_end,
+                   hipStream_t stream);
+
 /* Measurement helper, no counterpart in the reference: streams `bytes` from p (16-byte words,
  * nontemporal loads) with the given launch shape; used to measure the achievable HBM read
  * bandwidth that decode-step throughput is reported against. */

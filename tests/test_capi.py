@@ -49,6 +49,34 @@ def test_validation_rejects_without_launch():
                             1, 9, 32, 8, 128, 128, 128, None) == INVALID         # W*G > 32
     assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
                             1, 1, 32, 8, 128, 128, 100, None) == INVALID         # chunk % 32
+    # weight tiling: nr in {1, 2, 4, 8}, N a multiple of 16 * nr, K of 32, gate/up split = N / 2
+    assert L.dd_tile_weight(fake, fake, 64, 64, 3, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 48, 64, 2, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 48, 2, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 64, 4, 32, None) == INVALID
+    assert L.dd_tile_weight(None, fake, 64, 64, 2, 0, None) == INVALID
+
+
+def _step_args(**kw):
+    fake = ctypes.c_void_p(0x1000)
+    a = dict(layer_table=fake, L=36, embed=fake, lm_tiled=fake, final_norm=fake, cos_t=fake,
+             sin_t=fake, rope_rows=4096, tok=fake, pos=fake, h=fake, qbuf=fake, attn=fake,
+             mbuf=fake, logits=fake, ws=fake, counters=fake, err=fake, M=16, H=2560, NH=32,
+             NKV=8, I=9728, V=151936, cap=3072, eps=1e-6, chunk=256, phase_begin=0,
+             phase_end=2 + 5 * 36, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("bad", [
+    dict(M=17), dict(M=0), dict(NH=30), dict(chunk=100), dict(chunk=16), dict(H=2500),
+    dict(V=151930), dict(phase_end=3 + 5 * 36), dict(phase_begin=5, phase_end=5),
+    dict(tok=None), dict(counters=None), dict(NKV=64, NH=64),
+])
+def test_decode_step_validation(bad):
+    """dd_decode_step checks shapes and pointers before it queries the device or launches."""
+    L = dryft_amd.lib()
+    assert L.dd_decode_step(*_step_args(**bad)) == 1
 
 
 def test_host_side_sizing():
@@ -68,6 +96,8 @@ def test_host_side_sizing():
         assert L.dd_gemv_add_rmsnorm_ws_bytes(M, N, K, sk) == 4 * (sk * M * N + (M * N + 1) // 2 + -(-N // 16) * M)
         assert L.dd_gemv_counters(N) == -(-N // 16) + 1
     assert L.dd_argmax_ws_bytes(16, 151936) == 16 * 38 * 2 * 4
+    assert L.dd_tiled_bytes(6144, 2560) == 6144 * 2560 * 2
+    assert L.dd_step_counters() >= 1024 + 8192
     # attention: chunk multiple of 128, workspace covers every split of every row
     for B, cap in ((1, 640), (16, 3072), (16, 8192)):
         c = L.dd_attn_chunk(B, 8, cap)
