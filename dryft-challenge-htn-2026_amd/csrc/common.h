@@ -43,11 +43,16 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+// Global-memory pointers. Device pointers read from memory (layer tables) have no address space
+// the compiler can infer; without one it emits flat loads, which also count in lgkmcnt, so every
+// LDS wait would wait for the whole weight stream. These casts keep loads global (vmcnt only).
+typedef __attribute__((address_space(1))) const u32x4 gu32x4;
+
 // 16-byte global load; the pointer must be 16-byte aligned.
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(gu32x4*)p; }
 // 16-byte global load that streams past the caches (weights are read once per step).
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
-  return __builtin_nontemporal_load((const u32x4*)p);
+  return __builtin_nontemporal_load((gu32x4*)p);
 }
 
 // Wave-wide reductions (64 lanes). xor-shuffles give every lane the full result.

@@ -54,6 +54,34 @@ constexpr int E_TOKEN = 1, E_POS = 2, E_TIMEOUT = 4, E_GEOM = 8;
 // tiles per row group of each GEMV phase (log2)
 constexpr int LNR_QKV = 3, LNR_O = 2, LNR_GU = 1, LNR_D = 2, LNR_LM = 1;
 
+// Thread index read through an opaque move: values derived from it cannot be hoisted out of
+// the phase that computes them, so they do not stay live (in registers or spilled) across the
+// whole step.
+__device__ __forceinline__ int tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Wave index within the workgroup, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid() >> 6); }
+
+// Optional timing trace (compiled in only with -DDD_STEP_TRACE, for profiling builds): wall
+// clock (100 MHz) per workgroup at phase milestones, read back with dd_step_trace.
+constexpr int TR_PHASES = 192, TR_EVENTS = 4;
+#ifdef DD_STEP_TRACE
+__device__ unsigned long long g_trace[1024 * TR_PHASES * TR_EVENTS];
+#define STEP_TRACE(p, ev)                                                                    \
+  do {                                                                                      \
+    if (tid() == 0 && (p) < TR_PHASES)                                                      \
+      g_trace[((size_t)blockIdx.x * TR_PHASES + (p)) * TR_EVENTS + (ev)] = wall_clock64();   \
+  } while (0)
+#else
+#define STEP_TRACE(p, ev) \
+  do {                    \
+  } while (0)
+#endif
+
 struct Args {
   const int64_t* layers;             // [L][NFIELD] device pointers
   const bf16* embed;                 // [V][H] natural layout (gather)
@@ -63,10 +91,10 @@ struct Args {
   const bf16* sin_t;
   int64_t* tok;                      // [M] in: this step's tokens, out: next tokens
   int64_t* pos;                      // [M] per-row positions, += 1 at the end
-  bf16* h;                           // [M][H] residual stream
-  bf16* qbuf;                        // [M][NH][HD]
-  bf16* attn;                        // [M][NH*HD]
-  bf16* mbuf;                        // [M][I]
+  bf16* h;                           // [2L+1][M][H] residual stream, one slot per producer
+  bf16* qbuf;                        // [L][M][NH][HD]
+  bf16* attn;                        // [L][M][NH*HD]
+  bf16* mbuf;                        // [L][M][I]
   bf16* logits;                      // [M][V]
   float* ws;
   int* ctr;
@@ -74,12 +102,13 @@ struct Args {
   int L, M, H, NH, NKV, I, V, cap, rope_rows, chunk;
   float eps;
   int phase_begin, phase_end;
-  unsigned off_ss, off_part, off_att, off_am;   // workspace offsets (floats)
+  unsigned off_ss, off_part, off_att, off_am;   // workspace offsets (floats); ss: [2L+1][64][16]
   unsigned ws_floats;
 };
 
 struct Geo {                         // one GEMV phase for this workgroup
   const bf16* W;
+  rsrc_t wr;                         // this workgroup's steps s0 .. s1 of W (range-checked)
   int lnr, nk, ngroups, S, s0, s1;
 };
 
@@ -92,6 +121,7 @@ __device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr)
   g.S = g.ngroups * g.nk;
   g.s0 = (int)((long long)g.S * blockIdx.x / gridDim.x);
   g.s1 = (int)((long long)g.S * (blockIdx.x + 1) / gridDim.x);
+  g.wr = make_rsrc(W + ((size_t)g.s0 << (9 + lnr)), (unsigned)((g.s1 - g.s0) << (10 + lnr)));
   return g;
 }
 
@@ -100,21 +130,54 @@ __device__ __forceinline__ int wg_of_step(const Geo& g, int s) {
   return (int)((((long long)s + 1) * gridDim.x - 1) / g.S);
 }
 
+// Activation buffers are write-once within a launch: the residual stream h has one slot per
+// phase that produces it (embedding -> 0, O of layer l -> 2l+1, down of layer l -> 2l+2), q,
+// attention output and SiLU output one slot per layer. A slot is only read after the phase that
+// writes it (through to the device coherence point, sc1) and every cache is clean at launch
+// start, so no cache can hold a stale copy: readers use plain cached loads, and each XCD's L2
+// fetches a line once for all its workgroups.
+constexpr int SS_SLOT = 64 * MAXM;   // floats per sums-of-squares slot ([H/64 <= 64][16])
+__device__ __forceinline__ bf16* h_slot(const Args& a, int k) {
+  return a.h + (size_t)k * a.M * a.H;
+}
+__device__ __forceinline__ float* ss_slot(const Args& a, int k) {
+  return a.ws + a.off_ss + (size_t)k * SS_SLOT;
+}
+__device__ __forceinline__ bf16* q_slot(const Args& a, int l) {
+  return a.qbuf + (size_t)l * a.M * a.NH * HD;
+}
+__device__ __forceinline__ bf16* attn_slot(const Args& a, int l) {
+  return a.attn + (size_t)l * a.M * a.NH * HD;
+}
+__device__ __forceinline__ bf16* m_slot(const Args& a, int l) {
+  return a.mbuf + (size_t)l * a.M * a.I;
+}
+// plain (cached) 16-byte buffer load; out-of-range offsets read zeros
+__device__ __forceinline__ u32x4 ldb128(rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
 // first step of workgroup c's range (ranges of workgroups between two owners may be empty)
 __device__ __forceinline__ int step0_of(const Geo& g, int c) {
   return (int)((long long)g.S * c / gridDim.x);
 }
 
-// Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks).
+// Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks). The loads
+// are unconditional buffer loads through the workgroup's range descriptor: a step past the
+// range reads zeros without touching memory, and with no branches around the loads the compiler
+// waits for each buffer register on its own (vmcnt(n)) instead of draining the queue. The whole
+// offset is in the VGPR operand: the SGPR offset is not range-checked.
+constexpr int CP_NT = 2;   // buffer cache-policy bit nt (streaming)
+
 template <int NR>
 __device__ __forceinline__ void issue_batch(const Geo& g, int j0, u32x4 (&buf)[BATCH]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tid() & 63, wave = wave_id();
 #pragma unroll
   for (int b = 0; b < BATCH; ++b) {
     const int u = b / NR, t = b % NR;
-    const int s = g.s0 + wave + NWAVE * (j0 + u);
-    buf[b] = s < g.s1 ? ld16_stream(g.W + (((size_t)s * NR + t) << 9) + lane * 8)
-                      : u32x4{0u, 0u, 0u, 0u};
+    const int sl = wave + NWAVE * (j0 + u);          // step relative to s0
+    buf[b] = __builtin_amdgcn_raw_buffer_load_b128(g.wr, lane * 16 + ((sl * NR + t) << 10), 0,
+                                                   CP_NT);
   }
 }
 
@@ -133,6 +196,7 @@ struct Shared {
     } a;
   } u;
   float rs[MAXM];                             // per-row 1/rms of the staged x
+  float rsp[NTHR / MAXM][MAXM];               // partial sums of squares behind rs
   float ms[NWAVE][16];
   float ls[NWAVE][16];
   float bestv[MAXM];
@@ -160,7 +224,7 @@ struct GemvLds {
 __device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_s_barrier();
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     const int xcd = blockIdx.x & 7;
     const unsigned per = (unsigned)(gridDim.x >> 3);
     const unsigned old = __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR + 64 * (1 + xcd), 1u,
@@ -171,7 +235,7 @@ __device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
 }
 
 __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epoch) {
-  if (threadIdx.x == 0 && !sh.bail) {
+  if (tid() == 0 && !sh.bail) {
     const unsigned long long t0 = wall_clock64();
     while (__hip_atomic_load((unsigned*)a.ctr + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
            epoch * 8) {
@@ -189,55 +253,91 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
 // ---------------------------------------------------------------------------------------------
 // activation staging: x window [ksf, ksf + nw) (cyclic over nk k-steps) of an [M][K] source into
 // LDS rows of stride xrs bytes. NORM: x = bf16(bf16(h * r[m]) * lnw[k]) with r from the ss groups.
-__device__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g, int K,
-                        const bf16* src, const bf16* lnw) {
+// Every load of a batch is issued before the first is used (one memory latency per batch of
+// SBATCH items per thread), and the first batch is in flight while r is reduced.
+constexpr int SBATCH = 8;
+
+__device__ __forceinline__ unsigned stage_off(int it, int nw, int ksf, int nk, int K, int* lds) {
+  const int m = it / (nw * 4);
+  const int rem = it - m * nw * 4;
+  const int w = rem >> 2, e = rem & 3;
+  int ks = ksf + w;
+  if (ks >= nk) ks -= nk;
+  *lds = w * 64 + e * 16;
+  return (unsigned)((size_t)m * K + ks * 32 + e * 8);
+}
+
+__device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
+                                        int K, const bf16* src, const bf16* lnw, const float* ss) {
   const int M = a.M;
+  const int t = tid();
   int ksf = 0, nw = 0;
   if (g.s1 > g.s0) {
     ksf = g.s0 % g.nk;
     nw = min(g.s1 - g.s0, g.nk);
   }
   const int xrs = nw * 64 + 16;
-  if (lnw != nullptr && threadIdx.x < 64) {
-    // r[m] = 1/sqrt(sum_g ss[g][m] / H + eps); lanes 0..15 one row each, groups in order
-    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
-    const int m = threadIdx.x;
-    if (m < M) {
-      float t = 0.f;
-      for (int q = 0; q < a.H / SSG; ++q) t += ldc_f32(ssr, (unsigned)(q * MAXM + m) * 4);
-      sh.rs[m] = rsqrt_ieee(t / (float)a.H + a.eps);
+  const int items = M * nw * 4;
+  const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
+  u32x4 v[SBATCH], wv[SBATCH];
+  auto issue = [&](int base) {
+#pragma unroll
+    for (int b = 0; b < SBATCH; ++b) {
+      const int it = base + t + b * NTHR;
+      int lds;
+      const unsigned eo = it < items ? stage_off(it, nw, ksf, g.nk, K, &lds) : 0u;
+      v[b] = ldb128(sr, it < items ? eo * 2 : 0xfffffff0u);
+      if (lnw != nullptr)
+        wv[b] = it < items ? ld16(lnw + (eo % (unsigned)K)) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  issue(0);
+  if (lnw != nullptr) {
+    // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): thread (p, m) sums groups p, p + 32, ...; then
+    // row m adds the 32 partials in order
+    const int m = t & (MAXM - 1), p = t / MAXM;
+    float s = 0.f;
+    if (m < M)
+      for (int q = p; q < a.H / SSG; q += NTHR / MAXM) s += ss[q * MAXM + m];
+    sh.rsp[p][m] = s;
+    __syncthreads();
+    if (t < M) {
+      float r = 0.f;
+#pragma unroll 8
+      for (int q = 0; q < NTHR / MAXM; ++q) r += sh.rsp[q][t];
+      sh.rs[t] = rsqrt_ieee(r / (float)a.H + a.eps);
     }
   }
-  if (threadIdx.x == 0) {
+  if (t == 0) {
     sh.xrs = xrs;
     sh.xksf = ksf;
     sh.xnw = nw;
   }
   __syncthreads();
-  const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
-  const int items = M * nw * 4;
-  for (int it = threadIdx.x; it < items; it += NTHR) {
-    const int m = it / (nw * 4);
-    const int rem = it - m * nw * 4;
-    const int w = rem >> 2, e = rem & 3;
-    int ks = ksf + w;
-    if (ks >= g.nk) ks -= g.nk;
-    const int k = ks * 32 + e * 8;
-    u32x4 v = ldc_b128(sr, (unsigned)((size_t)m * K + k) * 2);
-    if (lnw != nullptr) {
-      const u32x4 wv = ld16(lnw + k);
-      const float r = sh.rs[m];
-      const unsigned hw[4] = {v.x, v.y, v.z, v.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
-      unsigned o[4];
+  for (int base = 0; base < items; base += SBATCH * NTHR) {
+    if (base > 0) issue(base);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const unsigned lo = f2bf(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]));
-        const unsigned hi = f2bf(rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
-        o[j] = lo | (hi << 16);
+    for (int b = 0; b < SBATCH; ++b) {
+      const int it = base + t + b * NTHR;
+      if (it >= items) break;
+      int lds;
+      stage_off(it, nw, ksf, g.nk, K, &lds);
+      const int m = it / (nw * 4);
+      u32x4 x = v[b];
+      if (lnw != nullptr) {
+        const float r = sh.rs[m];
+        const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+        unsigned o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const unsigned lo = f2bf(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]));
+          const unsigned hi = f2bf(rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
+          o[j] = lo | (hi << 16);
+        }
+        x = u32x4{o[0], o[1], o[2], o[3]};
       }
-      v = u32x4{o[0], o[1], o[2], o[3]};
+      *(u32x4*)(xb + m * xrs + lds) = x;
     }
-    *(u32x4*)(xb + m * xrs + w * 64 + e * 16) = v;
   }
   __syncthreads();
 }
@@ -246,7 +346,7 @@ __device__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo&
 // GEMV epilogues. `res[row][m]` holds the fp32 sums of the group's NR*16 weight rows.
 enum { EPI_QKV = 0, EPI_RES = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
-__device__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int head) {
+__device__ __forceinline__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int head) {
   // head < NH: q head; < NH+NKV: k head; else v head. 128 rows = the head's 128 dims.
   const int M = a.M;
   const int64_t* lp = a.layers + (size_t)layer * NFIELD;
@@ -254,7 +354,7 @@ __device__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int he
   const bf16* kn = (const bf16*)lp[F_KN];
   bf16* kc = (bf16*)lp[F_KC];
   bf16* vc = (bf16*)lp[F_VC];
-  const int t = threadIdx.x;
+  const int t = tid();
   const int m = t >> 5, j = t & 31;        // token m, dims {j, j+32, j+64, j+96}
   const bool act = m < M;
   int64_t p = act ? a.pos[m] : 0;
@@ -294,7 +394,7 @@ __device__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int he
     o4[q + 2] = rbf(rbf(n[q + 2] * c2) + rbf(n[q] * s2));
   }
   if (head < NH) {
-    const rsrc_t qr = make_rsrc(a.qbuf, (unsigned)((size_t)M * NH * HD * 2));
+    const rsrc_t qr = make_rsrc(q_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
     const size_t base = ((size_t)m * NH + head) * HD;
 #pragma unroll
     for (int q = 0; q < 4; ++q) stc_b16(qr, (unsigned)((base + j + 32 * q) * 2), f2bf(o4[q]));
@@ -306,40 +406,41 @@ __device__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int he
   }
 }
 
-__device__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp) {
-  // 64 residual columns grp*64 .. : h = bf16(h + bf16(sum)); ss[grp][m] = sum_c h^2
+__device__ __forceinline__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp, int hk) {
+  // 64 residual columns grp*64 .. : h[hk] = bf16(h[hk-1] + bf16(sum)); ss[hk][grp][m] = sum h^2
   const int M = a.M;
-  const int t = threadIdx.x;
+  const int t = tid();
   const int m = t >> 5, c2 = (t & 31) * 2;   // two columns per thread
-  const rsrc_t hr = make_rsrc(a.h, (unsigned)((size_t)M * a.H * 2));
+  const unsigned bytes = (unsigned)((size_t)M * a.H * 2);
+  const rsrc_t hin = make_rsrc(h_slot(a, hk - 1), bytes), hout = make_rsrc(h_slot(a, hk), bytes);
   float q = 0.f;
   if (m < M) {
     const unsigned off = (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2;
-    const unsigned hv2 = ldc_u32(hr, off);
+    const unsigned hv2 = __builtin_amdgcn_raw_buffer_load_b32(hin, off, 0, 0);
     const float h0 = rbf(lo_bf(hv2) + rbf(res[c2][m]));
     const float h1 = rbf(hi_bf(hv2) + rbf(res[c2 + 1][m]));
-    stc_u32(hr, off, (unsigned)f2bf(h0) | ((unsigned)f2bf(h1) << 16));
+    stc_u32(hout, off, (unsigned)f2bf(h0) | ((unsigned)f2bf(h1) << 16));
     q = h0 * h0 + h1 * h1;
   }
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
   if (m < M && (t & 31) == 0) {
-    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
+    const rsrc_t ssr = make_rsrc(ss_slot(a, hk), (unsigned)(SS_SLOT * 4));
     stc_f32(ssr, (unsigned)(grp * MAXM + m) * 4, q);
   }
 }
 
-__device__ void epi_silu(const Args& a, float (*res)[MAXM + 1], int grp) {
+__device__ __forceinline__ void epi_silu(const Args& a, float (*res)[MAXM + 1], int grp, int layer) {
   // rows 0..15: gate features grp*16.., rows 16..31: the matching up rows
   const int M = a.M;
-  const int t = threadIdx.x;
+  const int t = tid();
   if (t >= 16 * MAXM) return;
   const int m = t >> 4, f = t & 15;
   if (m >= M) return;
   const float g = rbf(res[f][m]);
   const float u = rbf(res[16 + f][m]);
   const float s = rbf(g / (1.0f + expf(-g)));
-  const rsrc_t mr = make_rsrc(a.mbuf, (unsigned)((size_t)M * a.I * 2));
+  const rsrc_t mr = make_rsrc(m_slot(a, layer), (unsigned)((size_t)M * a.I * 2));
   stc_b16(mr, (unsigned)((size_t)m * a.I + grp * 16 + f) * 2, f2bf(s * u));
 }
 
@@ -349,10 +450,10 @@ __device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
   return av > bv || (av == bv && ai < bi);
 }
 
-__device__ void epi_logits(const Args& a, Shared& sh, float (*res)[MAXM + 1], int grp) {
+__device__ __forceinline__ void epi_logits(const Args& a, Shared& sh, float (*res)[MAXM + 1], int grp) {
   // 32 vocab rows grp*32 ..; logits out + the workgroup's running argmax per token
   const int M = a.M;
-  const int t = threadIdx.x;
+  const int t = tid();
   const int m = t >> 5, v = t & 31;
   float val = -INFINITY;
   int idx = 0x7fffffff;
@@ -378,9 +479,9 @@ __device__ void epi_logits(const Args& a, Shared& sh, float (*res)[MAXM + 1], in
 // Reduce the waves' tiles of one row group, finish the group (directly, or through partials
 // when it is shared with other workgroups) and run the epilogue.
 template <int NR, int EPI>
-__device__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
+__device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
                             f32x4 (&acc)[NR]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
   GemvLds<NR> L(sh);
 #pragma unroll
@@ -392,7 +493,7 @@ __device__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, in
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes done (vmcnt untouched)
   __builtin_amdgcn_s_barrier();
   // res[row][m], row = t*16 + (lane/16)*4 + i of the D layout, m = lane % 16
-  for (int e = threadIdx.x; e < NR * 256; e += NTHR) {
+  for (int e = tid(); e < NR * 256; e += NTHR) {
     const int t = e >> 8, ln = (e >> 2) & 63, i = e & 3;
     float s = 0.f;
 #pragma unroll
@@ -410,7 +511,7 @@ __device__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, in
     const unsigned slot_floats = (unsigned)(rows * MAXM);
     const rsrc_t pr = make_rsrc(a.ws + a.off_part, (unsigned)(gridDim.x * 2 * slot_floats * 4));
     const int myslot = (grp == g.s0 / g.nk) ? 0 : 1;
-    for (int e = threadIdx.x; e < rows * M; e += NTHR) {
+    for (int e = tid(); e < rows * M; e += NTHR) {
       const int row = e / M, m = e - (e / M) * M;
       stc_f32(pr, ((blockIdx.x * 2 + myslot) * slot_floats + row * MAXM + m) * 4,
               L.res[row][m]);
@@ -420,87 +521,155 @@ __device__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, in
     for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
     finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
     if (finish) {
-      for (int e = threadIdx.x; e < rows * M; e += NTHR) {
-        const int row = e / M, m = e - (e / M) * M;
-        float s = 0.f;
-        for (int c = first; c <= last; ++c) {
+      // sum the contributors' partials in workgroup order, CB contributors' loads in flight at
+      // once (an empty contributor adds +0)
+      constexpr int EPT = (NR * 16 * MAXM + NTHR - 1) / NTHR;
+      constexpr int CB = 4;
+      float acc[EPT];
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) acc[i] = 0.f;
+      for (int c0 = first; c0 <= last; c0 += CB) {
+        float pv[EPT][CB];
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          const int c = c0 + j;
           const int cs0 = step0_of(g, c);
-          if (step0_of(g, c + 1) == cs0) continue;
+          const bool ok = c <= last && step0_of(g, c + 1) > cs0;
           const int slot = (grp == cs0 / g.nk) ? 0 : 1;
-          s += ldc_f32(pr, ((c * 2 + slot) * slot_floats + row * MAXM + m) * 4);
+#pragma unroll
+          for (int i = 0; i < EPT; ++i) {
+            const int e = tid() + i * NTHR;
+            const int row = e / M, m = e - row * M;
+            pv[i][j] = ok && e < rows * M
+                           ? ldc_f32(pr, ((c * 2 + slot) * slot_floats + row * MAXM + m) * 4)
+                           : 0.f;
+          }
         }
-        L.res[row][m] = s;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+#pragma unroll
+          for (int j = 0; j < CB; ++j) acc[i] += pv[i][j];
+      }
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) {
+        const int e = tid() + i * NTHR;
+        if (e < rows * M) L.res[e / M][e % M] = acc[i];
       }
       __syncthreads();
     }
   }
   if (finish) {
     if (EPI == EPI_QKV) epi_qkv(a, L.res, layer, grp);
-    else if (EPI == EPI_RES) epi_res(a, L.res, grp);
-    else if (EPI == EPI_SILU) epi_silu(a, L.res, grp);
+    else if (EPI == EPI_RES) epi_res(a, L.res, grp, layer);   // layer: output h slot
+    else if (EPI == EPI_SILU) epi_silu(a, L.res, grp, layer);
     else epi_logits(a, sh, L.res, grp);
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
 }
 
-// Consume this workgroup's steps of a GEMV phase. On entry cur/nxt hold (in flight) the wave's
-// batches 0 and 1. Returns with nothing in flight.
+// Consume U wave-steps j0 .. j0+U-1 from a prefetch buffer (static register indices: data still
+// in flight is never copied, so each MFMA waits only for its own loads). A wave's steps inside
+// one batch span at most two row groups (nk >= NWAVE * U): `cur` accumulates the oldest unflushed
+// group, `nxt` the one after it.
+template <int NR>
+__device__ __forceinline__ void gemv_consume(const Geo& g, const u32x4 (&buf)[BATCH], int j0,
+                                             int nmine, int gcur, const unsigned char* xrow_p,
+                                             int ksf, f32x4 (&cur)[NR], f32x4 (&nxt)[NR]) {
+  constexpr int U = BATCH / NR;
+  const int wave = wave_id();
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = j0 + u;
+    if (j < nmine) {
+      const int s = g.s0 + wave + NWAVE * j;
+      const int grp = s / g.nk;
+      int w = s - grp * g.nk - ksf;
+      if (w < 0) w += g.nk;
+      const u32x4 xv = *(const u32x4*)(xrow_p + w * 64);
+      if (grp == gcur) {
+#pragma unroll
+        for (int t = 0; t < NR; ++t) cur[t] = mfma16x16x32(buf[u * NR + t], xv, cur[t]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < NR; ++t) nxt[t] = mfma16x16x32(buf[u * NR + t], xv, nxt[t]);
+      }
+    }
+  }
+}
+
+// Flush the row groups this wave has moved past (all remaining ones when done): every wave of
+// the workgroup flushes every group of the range in order (flush_group synchronises them).
 template <int NR, int EPI>
-__device__ void gemv_phase(const Args& a, Shared& sh, const Geo& g, int layer,
-                           u32x4 (&cur)[BATCH], u32x4 (&nxt)[BATCH]) {
+__device__ __forceinline__ void gemv_flush_to(const Args& a, Shared& sh, const Geo& g, int layer,
+                                              int target, int seg0, int& flushed,
+                                              f32x4 (&cur)[NR], f32x4 (&nxt)[NR]) {
+  while (flushed < target) {
+    flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, cur);   // leaves cur zeroed
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      cur[t] = nxt[t];
+      nxt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    ++flushed;
+  }
+}
+
+// Consume this workgroup's steps of a GEMV phase. On entry A/B hold (in flight) the wave's
+// batches 0 and 1; batches alternate between them. Returns with nothing in flight.
+template <int NR, int EPI>
+__device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo& g, int layer,
+                                           u32x4 (&A)[BATCH], u32x4 (&B)[BATCH]) {
   constexpr int U = BATCH / NR;   // steps per batch
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
   const int nmine = g.s1 - g.s0 > wave ? (g.s1 - g.s0 - wave + NWAVE - 1) / NWAVE : 0;
   const int seg0 = g.s1 > g.s0 ? g.s0 / g.nk : 0;
   const int nseg = g.s1 > g.s0 ? (g.s1 - 1) / g.nk - seg0 + 1 : 0;
-  const unsigned char* xb = GemvLds<NR>(sh).x;
-  const int xrow = min(lane & 15, M - 1) * sh.xrs + (lane >> 4) * 16;
+  const unsigned char* xrow_p =
+      GemvLds<NR>(sh).x + min(lane & 15, M - 1) * sh.xrs + (lane >> 4) * 16;
   const int ksf = sh.xksf;
-  f32x4 acc[NR];
+  f32x4 cur[NR], nxt[NR];
 #pragma unroll
-  for (int t = 0; t < NR; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NR; ++t) {
+    cur[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    nxt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   int flushed = 0;
-  for (int j = 0;; ++j) {
-    int target = nseg, s = 0, grp = 0;
-    if (j < nmine) {
-      s = g.s0 + wave + NWAVE * j;
-      grp = s / g.nk;
-      target = grp - seg0;
+  // group of the wave's step j
+  auto grp_of = [&](int j) { return (g.s0 + wave + NWAVE * j) / g.nk - seg0; };
+  for (int j0 = 0;; j0 += 2 * U) {
+    if (j0 < nmine) {
+      gemv_consume<NR>(g, A, j0, nmine, seg0 + flushed, xrow_p, ksf, cur, nxt);
+      issue_batch<NR>(g, j0 + 2 * U, A);
+      __builtin_amdgcn_sched_barrier(0);    // keep the refill ahead of the next batch's MFMAs
+      gemv_flush_to<NR, EPI>(a, sh, g, layer, grp_of(min(j0 + U, nmine) - 1), seg0, flushed,
+                             cur, nxt);
     }
-    while (flushed < target) {
-      flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, acc);
-      ++flushed;
+    if (j0 + U < nmine) {
+      gemv_consume<NR>(g, B, j0 + U, nmine, seg0 + flushed, xrow_p, ksf, cur, nxt);
+      issue_batch<NR>(g, j0 + 3 * U, B);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (j >= nmine) break;
-    int w = s - grp * g.nk - ksf;
-    if (w < 0) w += g.nk;
-    const u32x4 xv = *(const u32x4*)(xb + xrow + w * 64);
-#pragma unroll
-    for (int t = 0; t < NR; ++t) acc[t] = mfma16x16x32(cur[t], xv, acc[t]);
-    if ((j + 1) % U == 0) {
-#pragma unroll
-      for (int b = 0; b < BATCH; ++b) cur[b] = nxt[b];
-      issue_batch<NR>(g, j + 1 + U, nxt);
-    } else {
-#pragma unroll
-      for (int b = 0; b + NR < BATCH; ++b) cur[b] = cur[b + NR];
-    }
+    const bool done = j0 + 2 * U >= nmine;
+    gemv_flush_to<NR, EPI>(a, sh, g, layer,
+                           done ? nseg : grp_of(min(j0 + 2 * U, nmine) - 1), seg0, flushed,
+                           cur, nxt);
+    if (done) break;
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // attention: units (row b, kv head, chunk of C keys); see attn.hip for the MFMA formulation.
-__device__ void attention_phase(const Args& a, Shared& sh, int layer) {
+__device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer) {
   const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV, C = a.chunk;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tid() & 63, wave = wave_id();
   const int l16 = lane & 15, g4 = lane >> 4;
   const int64_t* lp = a.layers + (size_t)layer * NFIELD;
   const bf16* kc = (const bf16*)lp[F_KC];
   const bf16* vc = (const bf16*)lp[F_VC];
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     int acc = 0;
     for (int b = 0; b < M; ++b) {
       sh.units[b] = acc;
@@ -515,10 +684,8 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
   const int u0 = (int)((long long)U * blockIdx.x / gridDim.x);
   const int u1 = (int)((long long)U * (blockIdx.x + 1) / gridDim.x);
   const size_t kvrow = (size_t)HD;
-  const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
-  const rsrc_t kr = make_rsrc(kc, kvbytes), vr = make_rsrc(vc, kvbytes);
-  const rsrc_t qr = make_rsrc(a.qbuf, (unsigned)((size_t)M * NH * HD * 2));
-  const rsrc_t orr = make_rsrc(a.attn, (unsigned)((size_t)M * NH * HD * 2));
+  const rsrc_t qr = make_rsrc(q_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
+  const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
   const int maxch = (a.cap + C - 1) / C;
   const unsigned wsrow = HD + 2;
   const rsrc_t pr = make_rsrc(a.ws + a.off_att, (unsigned)((size_t)MAXM * NKV * maxch * G * wsrow * 4));
@@ -537,7 +704,7 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
     u32x4 qreg[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      qreg[kb] = l16 < G ? ldc_b128(qr, (unsigned)((((size_t)b * NH + kvh * G + l16) * HD + kb * 32 + g4 * 8) * 2))
+      qreg[kb] = l16 < G ? ldb128(qr, (unsigned)((((size_t)b * NH + kvh * G + l16) * HD + kb * 32 + g4 * 8) * 2))
                          : u32x4{0u, 0u, 0u, 0u};
     f32x4 acc[8];
 #pragma unroll
@@ -547,8 +714,8 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
     const int nblk = (end - start + 31) >> 5;
     for (int bi = wave; bi < nblk; bi += NWAVE) {
       const int j0 = start + bi * 32;
-      // the block holding the newest key (written this launch) is read through sc1
-      const bool fresh = j0 + 31 >= (int)p0;
+      // K/V of this launch's position were written through to the coherence point in this
+      // layer's QKV phase and never read before in this launch: plain loads see them
       u32x4 kreg[2][4];
       u32x4 vreg[8];
 #pragma unroll
@@ -558,7 +725,7 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
           const size_t off = kvbase + (size_t)key * kvrow + kb * 32 + g4 * 8;
-          kreg[t][kb] = fresh ? ldc_b128(kr, (unsigned)(off * 2)) : ld16(kc + off);
+          kreg[t][kb] = ld16(kc + off);
         }
       }
 #pragma unroll
@@ -567,7 +734,7 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
         int key = j0 + (cc >> 4);
         key = key < a.cap ? key : a.cap - 1;
         const size_t off = kvbase + (size_t)key * kvrow + (cc & 15) * 8;
-        vreg[it] = fresh ? ldc_b128(vr, (unsigned)(off * 2)) : ld16(vc + off);
+        vreg[it] = ld16(vc + off);
       }
       f32x4 sc[2];
 #pragma unroll
@@ -643,7 +810,7 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
       sh.ls[wave][l16] = l_run;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < G * HD; e += NTHR) {
+    for (int e = tid(); e < G * HD; e += NTHR) {
       const int row = e / HD, d = e % HD;
       float Mx = -INFINITY;
 #pragma unroll
@@ -669,17 +836,40 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
       }
     }
     if (nch > 1 && arrive_last(a.ctr + C_ATT + bk, nch, &sh.flag)) {
-      for (int e = threadIdx.x; e < G * HD; e += NTHR) {
+      // log-sum-exp combine of the chunks, QB chunks' loads in flight at once
+      constexpr int QB = 8;
+      for (int e = tid(); e < G * HD; e += NTHR) {
         const int row = e / HD, d = e % HD;
         const unsigned pb0 = (unsigned)((((size_t)bk * maxch) * G + row) * wsrow) * 4;
         const unsigned cs = (unsigned)(G * wsrow) * 4;
         float Mx = -INFINITY;
-        for (int q = 0; q < nch; ++q) Mx = fmaxf(Mx, ldc_f32(pr, pb0 + q * cs + HD * 4));
+        for (int q0 = 0; q0 < nch; q0 += QB) {
+          float mv[QB];
+#pragma unroll
+          for (int j = 0; j < QB; ++j)
+            mv[j] = q0 + j < nch ? ldc_f32(pr, pb0 + (q0 + j) * cs + HD * 4) : -INFINITY;
+#pragma unroll
+          for (int j = 0; j < QB; ++j) Mx = fmaxf(Mx, mv[j]);
+        }
         float o = 0.f, l = 0.f;
-        for (int q = 0; q < nch; ++q) {
-          const float f = exp2f(ldc_f32(pr, pb0 + q * cs + HD * 4) - Mx);
-          o += ldc_f32(pr, pb0 + q * cs + d * 4) * f;
-          l += ldc_f32(pr, pb0 + q * cs + (HD + 1) * 4) * f;
+        for (int q0 = 0; q0 < nch; q0 += QB) {
+          float mv[QB], ov[QB], lv[QB];
+#pragma unroll
+          for (int j = 0; j < QB; ++j) {
+            const bool ok = q0 + j < nch;
+            const unsigned qb = pb0 + (q0 + j) * cs;
+            mv[j] = ok ? ldc_f32(pr, qb + HD * 4) : -INFINITY;
+            ov[j] = ok ? ldc_f32(pr, qb + d * 4) : 0.f;
+            lv[j] = ok ? ldc_f32(pr, qb + (HD + 1) * 4) : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < QB; ++j) {
+            if (q0 + j < nch) {
+              const float f = exp2f(mv[j] - Mx);
+              o += ov[j] * f;
+              l += lv[j] * f;
+            }
+          }
         }
         stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
       }
@@ -690,11 +880,11 @@ __device__ void attention_phase(const Args& a, Shared& sh, int layer) {
 
 // ---------------------------------------------------------------------------------------------
 // embedding gather: workgroup q < H/64 copies columns q*64.. of every row, stores ss[q][m]
-__device__ void embed_phase(const Args& a, Shared& sh) {
+__device__ __forceinline__ void embed_phase(const Args& a, Shared& sh) {
   const int M = a.M;
   const int q = blockIdx.x;
   if (q >= a.H / SSG) return;
-  const int t = threadIdx.x;
+  const int t = tid();
   const int m = t >> 5, c2 = (t & 31) * 2;
   float s = 0.f;
   if (m < M) {
@@ -704,14 +894,14 @@ __device__ void embed_phase(const Args& a, Shared& sh) {
       tk = 0;
     }
     const unsigned v2 = *(const unsigned*)(a.embed + (size_t)tk * a.H + q * SSG + c2);
-    const rsrc_t hr = make_rsrc(a.h, (unsigned)((size_t)M * a.H * 2));
+    const rsrc_t hr = make_rsrc(h_slot(a, 0), (unsigned)((size_t)M * a.H * 2));
     stc_u32(hr, (unsigned)((size_t)m * a.H + q * SSG + c2) * 2, v2);
     s = lo_bf(v2) * lo_bf(v2) + hi_bf(v2) * hi_bf(v2);
   }
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if (m < M && (t & 31) == 0) {
-    const rsrc_t ssr = make_rsrc(a.ws + a.off_ss, (unsigned)((a.H / SSG) * MAXM * 4));
+    const rsrc_t ssr = make_rsrc(ss_slot(a, 0), (unsigned)(SS_SLOT * 4));
     stc_f32(ssr, (unsigned)(q * MAXM + m) * 4, s);
   }
 }
@@ -744,27 +934,32 @@ __device__ __forceinline__ bool phase_geo(const Args& a, int p, Geo* g) {
 // One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, stage
 // the activation window, consume. The prefetch registers live only inside this call.
 template <int LNR, int EPI>
-__device__ void run_gemv(const Args& a, Shared& sh, const Geo& g, int layer, bool sync,
-                         unsigned epoch, int K, const bf16* src, const bf16* lnw) {
+__device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g, int p, int layer,
+                                         bool sync, unsigned epoch, int K, const bf16* src,
+                                         const bf16* lnw, const float* ss) {
   constexpr int NR = 1 << LNR;
-  u32x4 cur[BATCH], nxt[BATCH];
+  u32x4 A[BATCH], B[BATCH];
+  STEP_TRACE(p, 0);
   if (sync) bar_arrive(a, epoch);
-  issue_batch<NR>(g, 0, cur);
-  issue_batch<NR>(g, BATCH / NR, nxt);
+  issue_batch<NR>(g, 0, A);
+  issue_batch<NR>(g, BATCH / NR, B);
   if (sync) bar_wait(a, sh, epoch);
-  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw);
-  gemv_phase<NR, EPI>(a, sh, g, layer, cur, nxt);
+  STEP_TRACE(p, 1);
+  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss);
+  STEP_TRACE(p, 2);
+  gemv_phase<NR, EPI>(a, sh, g, layer, A, B);
+  STEP_TRACE(p, 3);
 }
 
 __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
   extern __shared__ unsigned char smem_raw[];
   Shared& sh = *(Shared*)smem_raw;
   unsigned epoch = 0;
-  if (threadIdx.x < MAXM) {
-    sh.bestv[threadIdx.x] = -INFINITY;
-    sh.besti[threadIdx.x] = 0x7fffffff;
+  if (tid() < MAXM) {
+    sh.bestv[tid()] = -INFINITY;
+    sh.besti[tid()] = 0x7fffffff;
   }
-  if (threadIdx.x == 0) sh.bail = 0;
+  if (tid() == 0) sh.bail = 0;
   __syncthreads();
   for (int p = a.phase_begin; p < a.phase_end; ++p) {
     int layer;
@@ -776,42 +971,50 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
     phase_geo(a, p, &g);
     switch (kind) {
       case P_QKV:
-        run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, layer, sync, epoch, a.H, a.h, (const bf16*)lp[F_LN1]);
+        run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer),
+                                   (const bf16*)lp[F_LN1], ss_slot(a, 2 * layer));
         break;
       case P_O:
-        run_gemv<LNR_O, EPI_RES>(a, sh, g, layer, sync, epoch, a.NH * HD, a.attn, nullptr);
+        run_gemv<LNR_O, EPI_RES>(a, sh, g, p, 2 * layer + 1, sync, epoch, a.NH * HD,
+                                 attn_slot(a, layer), nullptr, nullptr);
         break;
       case P_GU:
-        run_gemv<LNR_GU, EPI_SILU>(a, sh, g, layer, sync, epoch, a.H, a.h, (const bf16*)lp[F_LN2]);
+        run_gemv<LNR_GU, EPI_SILU>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer + 1),
+                                   (const bf16*)lp[F_LN2], ss_slot(a, 2 * layer + 1));
         break;
       case P_D:
-        run_gemv<LNR_D, EPI_RES>(a, sh, g, layer, sync, epoch, a.I, a.mbuf, nullptr);
+        run_gemv<LNR_D, EPI_RES>(a, sh, g, p, 2 * layer + 2, sync, epoch, a.I, m_slot(a, layer),
+                                 nullptr, nullptr);
         break;
       case P_LM:
-        run_gemv<LNR_LM, EPI_LOGITS>(a, sh, g, layer, sync, epoch, a.H, a.h, a.fnorm);
+        run_gemv<LNR_LM, EPI_LOGITS>(a, sh, g, p, 0, sync, epoch, a.H, h_slot(a, 2 * a.L), a.fnorm,
+                                     ss_slot(a, 2 * a.L));
         break;
       default:
+        STEP_TRACE(p, 0);
         if (sync) {
           bar_arrive(a, epoch);
           bar_wait(a, sh, epoch);
         }
+        STEP_TRACE(p, 1);
         if (kind == P_EMB) embed_phase(a, sh);
         else attention_phase(a, sh, layer);
+        STEP_TRACE(p, 3);
         break;
     }
     if (kind == P_LM) {
       // argmax over the workgroups' candidates; the last workgroup writes tok, advances pos
       const rsrc_t cr = make_rsrc(a.ws + a.off_am, (unsigned)(gridDim.x * MAXM * 2 * 4));
-      if (threadIdx.x < (unsigned)a.M) {
-        stc_f32(cr, (unsigned)((blockIdx.x * MAXM + threadIdx.x) * 2) * 4, sh.bestv[threadIdx.x]);
-        stc_u32(cr, (unsigned)((blockIdx.x * MAXM + threadIdx.x) * 2 + 1) * 4, (unsigned)sh.besti[threadIdx.x]);
+      if (tid() < (unsigned)a.M) {
+        stc_f32(cr, (unsigned)((blockIdx.x * MAXM + tid()) * 2) * 4, sh.bestv[tid()]);
+        stc_u32(cr, (unsigned)((blockIdx.x * MAXM + tid()) * 2 + 1) * 4, (unsigned)sh.besti[tid()]);
       }
       if (arrive_last(a.ctr + C_AM, gridDim.x, &sh.flag)) {
-        if (threadIdx.x < 64) {
+        if (tid() < 64) {
           for (int m = 0; m < a.M; ++m) {
             float bv = -INFINITY;
             int bi = 0x7fffffff;
-            for (int w = threadIdx.x; w < (int)gridDim.x; w += 64) {
+            for (int w = tid(); w < (int)gridDim.x; w += 64) {
               const float v = ldc_f32(cr, (unsigned)((w * MAXM + m) * 2) * 4);
               const int i = (int)ldc_u32(cr, (unsigned)((w * MAXM + m) * 2 + 1) * 4);
               if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
@@ -822,7 +1025,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
               const int oi = __shfl_xor(bi, o, 64);
               if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
             }
-            if (threadIdx.x == 0) {
+            if (tid() == 0) {
               a.tok[m] = bi;
               a.pos[m] += 1;
             }
@@ -834,7 +1037,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
   // exit: the last workgroup out resets the barrier counters for the next launch
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     const int old = __hip_atomic_fetch_add(a.ctr + C_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == (int)gridDim.x - 1) {
       __hip_atomic_store(a.ctr + C_BAR, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -902,10 +1105,10 @@ static int step_grid(int* G_out) {
 
 struct WsLayout { size_t ss, part, att, am, total; };
 
-static WsLayout ws_layout(int G, int NKV, int G_heads, int cap, int chunk) {
+static WsLayout ws_layout(int L, int G, int NKV, int G_heads, int cap, int chunk) {
   WsLayout w;
   w.ss = 0;
-  w.part = 1024;                                            // ss: [H/64 <= 64][16]
+  w.part = (size_t)(2 * L + 1) * SS_SLOT;                   // ss: [2L+1][H/64 <= 64][16]
   w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // 2 slots of <= 128 rows x 16
   const size_t maxch = (size_t)(cap + chunk - 1) / chunk;
   w.am = w.att + (size_t)MAXM * NKV * maxch * G_heads * (HD + 2);
@@ -920,10 +1123,10 @@ DD_API int dd_step_grid(void) {
 
 DD_API int dd_step_counters(void) { return C_TOTAL; }
 
-DD_API size_t dd_step_ws_bytes(int NH, int NKV, int cap, int chunk) {
+DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV, int cap, int chunk) {
   int G = 0;
-  if (step_grid(&G) != 0 || NKV < 1 || NH < NKV || cap < 1 || chunk < 32) return 0;
-  return ws_layout(G, NKV, NH / NKV, cap, chunk).total * sizeof(float);
+  if (L < 1 || NKV < 1 || NH < NKV || cap < 1 || chunk < 32 || step_grid(&G) != 0) return 0;
+  return ws_layout(L, G, NKV, NH / NKV, cap, chunk).total * sizeof(float);
 }
 
 DD_API size_t dd_tiled_bytes(int N, int K) { return (size_t)N * K * 2; }
@@ -941,6 +1144,39 @@ DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int 
   return launch_status();
 }
 
+// Model geometry the phases take (Qwen3 family, head_dim 128); G > 0 also checks that every
+// GEMV phase's staged activation window fits the LDS x buffer with that many workgroups.
+static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int G) {
+  if (!(M >= 1 && M <= MAXM && L >= 1 && NKV >= 1 && NH >= NKV && NH % NKV == 0 &&
+        NH / NKV <= 16))
+    return false;
+  if (MAXM * NKV > C_AM - C_ATT) return false;            // one combine counter per (row, kv head)
+  if (!(H % SSG == 0 && H / SSG <= 64 && I % 16 == 0 && V % 32 == 0)) return false;
+  const int K_of[5] = {H, NH * HD, H, I, H};
+  const int rows_of[5] = {(NH + 2 * NKV) * HD, H, 2 * I, H, V};
+  const int lnr_of[5] = {LNR_QKV, LNR_O, LNR_GU, LNR_D, LNR_LM};
+  for (int q = 0; q < 5; ++q) {
+    const int K = K_of[q], rows = rows_of[q], lnr = lnr_of[q];
+    if (K % 32 != 0 || rows % (16 << lnr) != 0) return false;
+    const int nk = K / 32;
+    if (nk < NWAVE * (BATCH >> lnr)) return false;       // a batch spans at most two row groups
+    if ((rows >> (4 + lnr)) > C_ATT - C_GROUP) return false;
+    if (G > 0) {
+      const long long S = (long long)(rows >> (4 + lnr)) * nk;
+      const long long per = (S + G - 1) / G;
+      const long long nw = per < nk ? per : nk;
+      if ((nw * 64 + 16) * M > (long long)x_capacity(1 << lnr)) return false;
+    }
+  }
+  return true;
+}
+
+DD_API int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M) {
+  int G = 0;
+  if (step_grid(&G) != 0) return 0;
+  return geometry_ok(L, H, NH, NKV, I, V, M, G) ? 1 : 0;
+}
+
 DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,
                           const void* final_norm, const void* cos_t, const void* sin_t,
                           int rope_rows, int64_t* tok, int64_t* pos, void* h, void* qbuf,
@@ -949,33 +1185,14 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
                           int chunk, int phase_begin, int phase_end, hipStream_t stream) {
   DD_REQUIRE(layer_table && embed && lm_tiled && final_norm && cos_t && sin_t && tok && pos);
   DD_REQUIRE(h && qbuf && attn && mbuf && logits && ws && counters && err);
-  DD_REQUIRE(M >= 1 && M <= MAXM && L >= 1 && NKV >= 1 && NH % NKV == 0 && NH / NKV <= 16);
-  DD_REQUIRE(MAXM * NKV <= C_AM - C_ATT);   // one combine counter per (row, kv head)
-  // geometry the phases assume (Qwen3 family with head_dim 128)
-  DD_REQUIRE(H % SSG == 0 && H / SSG <= 64 && H % 32 == 0 && I % 32 == 0 && I % 16 == 0);
-  DD_REQUIRE(V % 32 == 0 && ((NH + 2 * NKV) * HD) % 128 == 0 && H % 64 == 0);
+  DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, 0));
   DD_REQUIRE(chunk >= 32 && chunk % 32 == 0 && cap >= 1 && rope_rows >= 1);
   DD_REQUIRE(phase_begin >= 0 && phase_begin < phase_end && phase_end <= 2 + 5 * L);
   int G = 0;
   const int e = step_grid(&G);
   if (e != 0) return e;
-  // the staged activation window of every GEMV phase must fit the LDS x buffer
-  {
-    const int K_of[4] = {H, NH * HD, H, I};
-    const int rows_of[4] = {(NH + 2 * NKV) * HD, H, 2 * I, H};
-    const int lnr_of[4] = {LNR_QKV, LNR_O, LNR_GU, LNR_D};
-    for (int q = 0; q < 5; ++q) {
-      const int K = q < 4 ? K_of[q] : H;
-      const int rows = q < 4 ? rows_of[q] : V;
-      const int lnr = q < 4 ? lnr_of[q] : LNR_LM;
-      const long long S = (long long)(rows >> (4 + lnr)) * (K / 32);
-      const long long per = (S + G - 1) / G;
-      const long long nw = per < K / 32 ? per : K / 32;
-      DD_REQUIRE((nw * 64 + 16) * M <= (long long)x_capacity(1 << lnr));
-      DD_REQUIRE((rows >> (4 + lnr)) <= 8192);
-    }
-  }
-  const WsLayout w = ws_layout(G, NKV, NH / NKV, cap, chunk);
+  DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, G));
+  const WsLayout w = ws_layout(L, G, NKV, NH / NKV, cap, chunk);
   Args a;
   a.layers = layer_table;
   a.embed = (const bf16*)embed;
@@ -1005,3 +1222,10 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   hipLaunchKernelGGL(decode_step_kernel, dim3(G), dim3(NTHR), sizeof(Shared), stream, a);
   return launch_status();
 }
+
+#ifdef DD_STEP_TRACE
+// Profiling builds only: copy the timing trace ([1024][192][4] u64) to host memory.
+DD_API int dd_step_trace(void* host, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif

@@ -43,8 +43,10 @@ class FusedStep:
         if e.hd != HD:
             raise RuntimeError(f"fused decode step needs head_dim {HD}, got {e.hd}")
         self.H = e.embed.shape[1]
-        self.V = e.embed.shape[0] if e.lm_head is e.embed else e.lm_head.shape[0]
+        self.V = e.lm_head.shape[0]
         self.I = e.layers[0].wd.shape[1]
+        if not self.L.dd_step_supported(e.L, self.H, e.nh, e.nkv, self.I, self.V, MAXM):
+            raise RuntimeError("dd_step_supported: model geometry not taken by the fused step")
         with torch.no_grad():
             for l in e.layers:
                 l.wqkv_t = self._tile(l.wqkv, NR_QKV)
@@ -72,12 +74,15 @@ class FusedStep:
         B, H, I, V = st.B, self.H, self.I, self.V
         bf = dict(dtype=torch.bfloat16, device=dev)
         f = _State()
-        f.h = torch.empty(B, H, **bf)
-        f.qbuf = torch.empty(B, e.nh * HD, **bf)
-        f.attn = torch.empty(B, e.nh * HD, **bf)
-        f.mbuf = torch.empty(B, I, **bf)
+        L = e.L
+        # write-once activation slots (see dd_decode_step): h per producing phase, the others
+        # per layer
+        f.h = torch.empty(2 * L + 1, B, H, **bf)
+        f.qbuf = torch.empty(L, B, e.nh * HD, **bf)
+        f.attn = torch.empty(L, B, e.nh * HD, **bf)
+        f.mbuf = torch.empty(L, B, I, **bf)
         f.logits = torch.empty(B, V, **bf)
-        ws = self.L.dd_step_ws_bytes(e.nh, e.nkv, st.cap, CHUNK)
+        ws = self.L.dd_step_ws_bytes(L, e.nh, e.nkv, st.cap, CHUNK)
         if ws == 0:
             raise RuntimeError("dd_step_ws_bytes rejected the shape")
         f.ws = torch.empty(ws // 4, dtype=torch.float32, device=dev)

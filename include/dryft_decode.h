@@ -136,8 +136,12 @@ size_t dd_argmax_ws_bytes(int M, int V);
  * tile 0 = gate rows g*16.., tile 1 = up rows gate_up_I + g*16... nr per matrix: wqkv 8,
  * wo 4, wgu 2 (gate_up_I = I), wd 4, lm_head 2. dst holds dd_tiled_bytes(N, K). */
 int dd_step_grid(void);
+/* 1 when dd_decode_step takes this model geometry for up to M rows on the current device
+ * (head_dim 128; per GEMV phase at least 8 wave-batches of 32-column steps per row group:
+ * hidden >= 1024, heads * 128 >= 512, intermediate >= 512; vocab % 32 == 0), else 0. */
+int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M);
 int dd_step_counters(void);
-size_t dd_step_ws_bytes(int NH, int NKV, int cap, int chunk);
+size_t dd_step_ws_bytes(int L, int NH, int NKV, int cap, int chunk);
 size_t dd_tiled_bytes(int N, int K);
 int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
                    hipStream_t stream);
@@ -146,9 +150,12 @@ int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up
  * 2 wgu (tiled), 3 wd (tiled), 4 input_layernorm, 5 post_attention_layernorm, 6 q_norm,
  * 7 k_norm, 8 K cache, 9 V cache ([M, NKV, cap, 128] each); 10..15 unused.
  * tok/pos: [M] int64 (in: this step's tokens and positions; out: the argmax tokens, pos + 1).
- * Buffers: h [M, H], qbuf [M, NH, 128], attn [M, NH*128], mbuf [M, I], logits [M, V] (bf16,
- * logits hold the step's lm_head output afterwards); ws dd_step_ws_bytes; counters
- * dd_step_counters() zeroed ints. chunk: keys per attention split (multiple of 32).
+ * Activation buffers (bf16), written once per launch (one slot per producing phase, so they
+ * are read with plain cached loads): h [2L+1, M, H] (slot 0 embedding, 2l+1 after layer l's
+ * O projection, 2l+2 after its down projection), qbuf [L, M, NH, 128], attn [L, M, NH*128],
+ * mbuf [L, M, I]; logits [M, V] hold the step's lm_head output afterwards. ws:
+ * dd_step_ws_bytes; counters: dd_step_counters() zeroed ints. chunk: keys per attention split
+ * (multiple of 32).
  * phase_begin/phase_end select a sub-range of the 2 + 5L phases (0 embedding, 1 + 5l + {0 QKV,
  * 1 attention, 2 O, 3 gate/up, 4 down}, 1 + 5L lm_head/argmax); a full step is 0 .. 2 + 5L. */
 int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,

@@ -124,19 +124,33 @@ def _step_parity(ref, eng, prompts, n_steps, seed):
     return worst, flips
 
 
-TINY = synth.qwen3_config(vocab_size=512, hidden_size=256, intermediate_size=192,
-                          num_hidden_layers=3, num_attention_heads=8, num_key_value_heads=2,
-                          head_dim=128)
+# smallest geometry class the fused step takes; its QKV phase has fewer 32-column steps (6 heads x
+# 32 = 192) than there are workgroups, so some workgroups own no steps of it
+SMALL = synth.qwen3_config(vocab_size=1024, hidden_size=1024, intermediate_size=512,
+                           num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=1,
+                           head_dim=128)
 
 
-def test_fused_step_tiny_ragged(cuda):
-    """Small model: fewer k-steps than workgroups in every GEMV phase (empty workgroup ranges),
-    ragged per-row positions."""
-    ref, eng = _engine(TINY, seed=5)
+def test_fused_step_small_ragged(cuda):
+    """Small model (empty workgroup ranges in the QKV phase), ragged per-row positions."""
+    ref, eng = _engine(SMALL, seed=5)
     g = torch.Generator().manual_seed(1)
-    prompts = [torch.randint(0, 512, (L,), generator=g).tolist() for L in (5, 40, 17, 100)]
+    prompts = [torch.randint(0, 1024, (L,), generator=g).tolist() for L in (5, 40, 17, 100)]
     worst, flips = _step_parity(ref, eng, prompts, 4, seed=2)
-    print(f"tiny: worst logit diff {worst:.4f}, near-tie flips {flips}")
+    print(f"small: worst logit diff {worst:.4f}, near-tie flips {flips}")
+
+
+def test_fused_step_unsupported_geometry(cuda):
+    """Geometries the fused step does not take are reported by dd_step_supported, and the engine
+    then decodes with the per-op kernels."""
+    from dryft_amd.engine import Engine
+    tiny = synth.qwen3_config(vocab_size=512, hidden_size=256, intermediate_size=192,
+                              num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                              head_dim=128)
+    w = synth.random_weights(tiny, seed=0)
+    eng = Engine.from_state_dict(tiny, {k: v.cuda() for k, v in w.items()}, selftest=False)
+    assert eng.step is None
+    assert eng._new_state(2, 128).fused is None
 
 
 def test_fused_step_qwen3_width_b16(cuda):
@@ -180,13 +194,15 @@ def test_fused_phases_per_kernel(cuda):
     kc0, vc0 = st.kc[0].cpu(), st.vc[0].cpu()
     cpu = lambda t: t.cpu()
 
+    # the step's activation buffers are write-once slots: h[0] embedding, h[1] after O, h[2]
+    # after down; q, attention output and SiLU output one slot per layer
     eng.step.run(st, 0, 2)                                   # embedding + QKV
-    h = cpu(f.h)
+    h = cpu(f.h[0])
     assert torch.equal(h.view(torch.int16), ref.embed[tok].view(torch.int16))
     rkc, rvc = kc0.clone(), vc0.clone()
     qkv = ops.linear(ops.rms(h, rl.ln1), rl.wqkv)
     q = ops.qkv_post_rows(qkv, rl, rkc, rvc, pos)            # [B, nh, 1, hd]
-    _close(cpu(f.qbuf).view(B, eng.nh, 128), q.reshape(B, eng.nh, 128), "q (norm + rope)")
+    _close(cpu(f.qbuf[0]).view(B, eng.nh, 128), q.reshape(B, eng.nh, 128), "q (norm + rope)")
     for name, c, c0, rc in (("K", st.kc[0], kc0, rkc), ("V", st.vc[0], vc0, rvc)):
         c = c.cpu()
         changed = (c != c0).any(-1).any(1)
@@ -197,23 +213,23 @@ def test_fused_phases_per_kernel(cuda):
         _close(c.gather(2, idx), rc.gather(2, idx), f"{name} write")
 
     eng.step.run(st, 2, 3)                                   # attention
-    qg = cpu(f.qbuf).view(B, eng.nh, 1, 128)
+    qg = cpu(f.qbuf[0]).view(B, eng.nh, 1, 128)
     o = ops.attn_decode_rows(qg, st.kc[0].cpu(), st.vc[0].cpu(), pos)
-    _close(cpu(f.attn), o, "attention")
+    _close(cpu(f.attn[0]), o, "attention")
 
-    attn = cpu(f.attn)
+    attn = cpu(f.attn[0])
     eng.step.run(st, 3, 4)                                   # O + residual
-    h1 = cpu(f.h)
+    h1 = cpu(f.h[1])
     want_h1, _ = ops.linear_add_norm(attn, rl.wo, h, rl.ln2)
     _close(h1, want_h1, "O + residual")
 
     eng.step.run(st, 4, 5)                                   # gate/up + SiLU (RMSNorm on the way in)
     m = ops.gate_up_silu(ops.rms(h1, rl.ln2), rl.wgu)
-    _close(cpu(f.mbuf), m, "gate/up + SiLU")
+    _close(cpu(f.mbuf[0]), m, "gate/up + SiLU")
 
-    mb = cpu(f.mbuf)
+    mb = cpu(f.mbuf[0])
     eng.step.run(st, 5, 6)                                   # down + residual
-    h2 = cpu(f.h)
+    h2 = cpu(f.h[2])
     want_h2, _ = ops.linear_add_norm(mb, rl.wd, h1, ref.norm)
     _close(h2, want_h2, "down + residual")
 
@@ -256,7 +272,7 @@ def test_fused_step_vs_per_op(cuda):
 def test_fused_step_error_flags(cuda):
     """A position outside the cache sets flag 2 and writes nothing; an out-of-range token sets
     flag 1 (row uses token 0). Nothing faults; the counters are left zeroed."""
-    _, eng = _engine(TINY, seed=5)
+    _, eng = _engine(SMALL, seed=5)
     st = eng._new_state(2, 128)
     eng._prefill([[1, 2, 3], [4, 5, 6, 7]], st)
     kc0 = [k.clone() for k in st.kc]
