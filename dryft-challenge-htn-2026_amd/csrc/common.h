@@ -22,12 +22,14 @@ typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
 __device__ __forceinline__ float bf2f(bf16 v) { return __uint_as_float(((unsigned)v) << 16); }
 
-// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quietened).
-__device__ __forceinline__ bf16 f2bf(float f) {
-  unsigned u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16)(u >> 16);
+// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quietened). gfx950 converts in hardware
+// (v_cvt_pk_bf16_f32), two values per instruction when they are packed together.
+__device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, (__bf16)f); }
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+// two fp32 -> packed bf16 pair (lo in bits 0..15)
+__device__ __forceinline__ unsigned pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(unsigned, bf16x2_t{(__bf16)lo, (__bf16)hi});
 }
 
 // Round an fp32 value to the nearest bf16 value, returned as fp32.

@@ -52,7 +52,7 @@ constexpr int C_TOTAL = C_AM + 64;
 constexpr int E_TOKEN = 1, E_POS = 2, E_TIMEOUT = 4, E_GEOM = 8;
 
 // tiles per row group of each GEMV phase (log2)
-constexpr int LNR_QKV = 3, LNR_O = 2, LNR_GU = 1, LNR_D = 2, LNR_LM = 1;
+constexpr int LNR_QKV = 1, LNR_O = 2, LNR_GU = 1, LNR_D = 2, LNR_LM = 1;
 
 // Thread index read through an opaque move: values derived from it cannot be hoisted out of
 // the phase that computes them, so they do not stay live (in registers or spilled) across the
@@ -68,7 +68,7 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 
 // Optional timing trace (compiled in only with -DDD_STEP_TRACE, for profiling builds): wall
 // clock (100 MHz) per workgroup at phase milestones, read back with dd_step_trace.
-constexpr int TR_PHASES = 192, TR_EVENTS = 4;
+constexpr int TR_PHASES = 192, TR_EVENTS = 8;
 #ifdef DD_STEP_TRACE
 __device__ unsigned long long g_trace[1024 * TR_PHASES * TR_EVENTS];
 #define STEP_TRACE(p, ev)                                                                    \
@@ -92,47 +92,53 @@ struct Args {
   int64_t* tok;                      // [M] in: this step's tokens, out: next tokens
   int64_t* pos;                      // [M] per-row positions, += 1 at the end
   bf16* h;                           // [2L+1][M][H] residual stream, one slot per producer
-  bf16* qbuf;                        // [L][M][NH][HD]
+  bf16* qkv;                         // [L][M][(NH + 2 NKV) * HD] raw q|k|v
   bf16* attn;                        // [L][M][NH*HD]
   bf16* mbuf;                        // [L][M][I]
   bf16* logits;                      // [M][V]
   float* ws;
   int* ctr;
   int* err;
-  int L, M, H, NH, NKV, I, V, cap, rope_rows, chunk;
+  int L, M, H, NH, NKV, I, V, cap, rope_rows;
   float eps;
   int phase_begin, phase_end;
   unsigned off_ss, off_part, off_att, off_am;   // workspace offsets (floats); ss: [2L+1][64][16]
   unsigned ws_floats;
 };
 
+// The steps of a phase are split into equal contiguous workgroup ranges in units of `unit`
+// steps: 1 (stream-K: equal bytes per workgroup; a row group cut between workgroups is finished
+// by its last contributor) or nk (whole row groups per workgroup: no cross-workgroup partials,
+// balanced when there are many groups per workgroup or the epilogue needs the whole group).
 struct Geo {                         // one GEMV phase for this workgroup
   const bf16* W;
   rsrc_t wr;                         // this workgroup's steps s0 .. s1 of W (range-checked)
-  int lnr, nk, ngroups, S, s0, s1;
+  int lnr, nk, ngroups, S, unit, nu, s0, s1;
 };
 
-__device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr) {
+__device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr, bool whole) {
   Geo g;
   g.W = W;
   g.lnr = lnr;
   g.nk = K >> 5;
   g.ngroups = rows >> (4 + lnr);
   g.S = g.ngroups * g.nk;
-  g.s0 = (int)((long long)g.S * blockIdx.x / gridDim.x);
-  g.s1 = (int)((long long)g.S * (blockIdx.x + 1) / gridDim.x);
+  g.unit = whole ? g.nk : 1;
+  g.nu = whole ? g.ngroups : g.S;
+  g.s0 = (int)((long long)g.nu * blockIdx.x / gridDim.x) * g.unit;
+  g.s1 = (int)((long long)g.nu * (blockIdx.x + 1) / gridDim.x) * g.unit;
   g.wr = make_rsrc(W + ((size_t)g.s0 << (9 + lnr)), (unsigned)((g.s1 - g.s0) << (10 + lnr)));
   return g;
 }
 
 // workgroup owning global step s
 __device__ __forceinline__ int wg_of_step(const Geo& g, int s) {
-  return (int)((((long long)s + 1) * gridDim.x - 1) / g.S);
+  return (int)((((long long)(s / g.unit) + 1) * gridDim.x - 1) / g.nu);
 }
 
 // Activation buffers are write-once within a launch: the residual stream h has one slot per
-// phase that produces it (embedding -> 0, O of layer l -> 2l+1, down of layer l -> 2l+2), q,
-// attention output and SiLU output one slot per layer. A slot is only read after the phase that
+// phase that produces it (embedding -> 0, O of layer l -> 2l+1, down of layer l -> 2l+2), raw
+// q|k|v, attention output and SiLU output one slot per layer. A slot is only read after the phase that
 // writes it (through to the device coherence point, sc1) and every cache is clean at launch
 // start, so no cache can hold a stale copy: readers use plain cached loads, and each XCD's L2
 // fetches a line once for all its workgroups.
@@ -143,8 +149,8 @@ __device__ __forceinline__ bf16* h_slot(const Args& a, int k) {
 __device__ __forceinline__ float* ss_slot(const Args& a, int k) {
   return a.ws + a.off_ss + (size_t)k * SS_SLOT;
 }
-__device__ __forceinline__ bf16* q_slot(const Args& a, int l) {
-  return a.qbuf + (size_t)l * a.M * a.NH * HD;
+__device__ __forceinline__ bf16* qkv_slot(const Args& a, int l) {
+  return a.qkv + (size_t)l * a.M * (a.NH + 2 * a.NKV) * HD;
 }
 __device__ __forceinline__ bf16* attn_slot(const Args& a, int l) {
   return a.attn + (size_t)l * a.M * a.NH * HD;
@@ -159,7 +165,7 @@ __device__ __forceinline__ u32x4 ldb128(rsrc_t r, unsigned off) {
 
 // first step of workgroup c's range (ranges of workgroups between two owners may be empty)
 __device__ __forceinline__ int step0_of(const Geo& g, int c) {
-  return (int)((long long)g.S * c / gridDim.x);
+  return (int)((long long)g.nu * c / gridDim.x) * g.unit;
 }
 
 // Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks). The loads
@@ -187,12 +193,15 @@ constexpr int GBUF = 112 * 1024;
 constexpr int RES_BYTES = 8 * 16 * (MAXM + 1) * 4;
 __host__ __device__ constexpr int x_capacity(int NR) { return GBUF - NR * NWAVE * 256 * 4 - RES_BYTES; }
 
+constexpr int LNW_KS = 128;                   // k-steps of the norm weight staged in LDS
+
 struct Shared {
   union {
     unsigned char g[GBUF];                    // GEMV phases (see GemvLds)
     struct {                                  // attention
       bf16 v[NWAVE][32][HD + 8];
       float mrg[NWAVE][16][HD];
+      bf16 qn[32][HD];                        // normalised, rotated query heads of the segments
     } a;
   } u;
   float rs[MAXM];                             // per-row 1/rms of the staged x
@@ -206,6 +215,9 @@ struct Shared {
   int xrs;                                    // staged x row stride (bytes)
   int xksf, xnw;                              // staged window: first k-step, width
   int units[MAXM + 1];                        // attention unit prefix sums
+  int seg[32][4];                             // attention segments: b, kvh, first block, blocks
+  int nseg, segnext;
+  bf16 lnw[LNW_KS * 32];                      // staged norm weight window (<= LNW_KS k-steps)
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -254,8 +266,9 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
 // activation staging: x window [ksf, ksf + nw) (cyclic over nk k-steps) of an [M][K] source into
 // LDS rows of stride xrs bytes. NORM: x = bf16(bf16(h * r[m]) * lnw[k]) with r from the ss groups.
 // Every load of a batch is issued before the first is used (one memory latency per batch of
-// SBATCH items per thread), and the first batch is in flight while r is reduced.
-constexpr int SBATCH = 8;
+// SBATCH items per thread), and the first batch is in flight while r is reduced. The norm
+// weight window (the same for every row) is staged once into LDS.
+constexpr int SBATCH = 12;
 
 __device__ __forceinline__ unsigned stage_off(int it, int nw, int ksf, int nk, int K, int* lds) {
   const int m = it / (nw * 4);
@@ -268,7 +281,8 @@ __device__ __forceinline__ unsigned stage_off(int it, int nw, int ksf, int nk, i
 }
 
 __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
-                                        int K, const bf16* src, const bf16* lnw, const float* ss) {
+                                        int K, const bf16* src, const bf16* lnw, const float* ss,
+                                        int p) {
   const int M = a.M;
   const int t = tid();
   int ksf = 0, nw = 0;
@@ -279,20 +293,31 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
   const int xrs = nw * 64 + 16;
   const int items = M * nw * 4;
   const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
-  u32x4 v[SBATCH], wv[SBATCH];
+  // every workgroup of an XCD may stage the same window: start each one at a different item so
+  // concurrent requests spread over different cache lines
+  const int rot = items > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) % (unsigned)items) : 0;
+  auto item_at = [&](int j) { const int it = j + rot; return it < items ? it : it - items; };
+  u32x4 v[SBATCH];
   auto issue = [&](int base) {
 #pragma unroll
     for (int b = 0; b < SBATCH; ++b) {
-      const int it = base + t + b * NTHR;
+      const int j = base + t + b * NTHR;
       int lds;
-      const unsigned eo = it < items ? stage_off(it, nw, ksf, g.nk, K, &lds) : 0u;
-      v[b] = ldb128(sr, it < items ? eo * 2 : 0xfffffff0u);
-      if (lnw != nullptr)
-        wv[b] = it < items ? ld16(lnw + (eo % (unsigned)K)) : u32x4{0u, 0u, 0u, 0u};
+      const unsigned eo = j < items ? stage_off(item_at(j), nw, ksf, g.nk, K, &lds) : 0u;
+      v[b] = ldb128(sr, j < items ? eo * 2 : 0xfffffff0u);
     }
   };
   issue(0);
+  STEP_TRACE(p, 4);
+  // a norm window beyond the LDS copy (only with fewer workgroups than the window needs) is
+  // read from global memory per item instead
+  const bool lnw_lds = lnw != nullptr && nw <= LNW_KS;
   if (lnw != nullptr) {
+    if (lnw_lds && t < nw * 4) {
+      int ks = ksf + (t >> 2);
+      if (ks >= g.nk) ks -= g.nk;
+      *(u32x4*)&sh.lnw[t * 8] = ld16(lnw + ks * 32 + (t & 3) * 8);
+    }
     // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): thread (p, m) sums groups p, p + 32, ...; then
     // row m adds the 32 partials in order
     const int m = t & (MAXM - 1), p = t / MAXM;
@@ -308,6 +333,7 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
       sh.rs[t] = rsqrt_ieee(r / (float)a.H + a.eps);
     }
   }
+  STEP_TRACE(p, 5);
   if (t == 0) {
     sh.xrs = xrs;
     sh.xksf = ksf;
@@ -318,27 +344,28 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
     if (base > 0) issue(base);
 #pragma unroll
     for (int b = 0; b < SBATCH; ++b) {
-      const int it = base + t + b * NTHR;
-      if (it >= items) break;
+      const int j = base + t + b * NTHR;
+      if (j >= items) break;
+      const int it = item_at(j);
       int lds;
-      stage_off(it, nw, ksf, g.nk, K, &lds);
+      const unsigned eo = stage_off(it, nw, ksf, g.nk, K, &lds);
       const int m = it / (nw * 4);
       u32x4 x = v[b];
       if (lnw != nullptr) {
         const float r = sh.rs[m];
-        const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+        const u32x4 wv = lnw_lds ? *(const u32x4*)&sh.lnw[(lds >> 4) * 8]
+                                 : ld16(lnw + (eo - (unsigned)m * K));
+        const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
         unsigned o[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const unsigned lo = f2bf(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]));
-          const unsigned hi = f2bf(rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
-          o[j] = lo | (hi << 16);
-        }
+        for (int j = 0; j < 4; ++j)
+          o[j] = pk_bf16(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]), rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
         x = u32x4{o[0], o[1], o[2], o[3]};
       }
       *(u32x4*)(xb + m * xrs + lds) = x;
     }
   }
+  STEP_TRACE(p, 6);
   __syncthreads();
 }
 
@@ -346,63 +373,17 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
 // GEMV epilogues. `res[row][m]` holds the fp32 sums of the group's NR*16 weight rows.
 enum { EPI_QKV = 0, EPI_RES = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
-__device__ __forceinline__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int head) {
-  // head < NH: q head; < NH+NKV: k head; else v head. 128 rows = the head's 128 dims.
+__device__ __forceinline__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int grp) {
+  // raw q|k|v rows grp*32 .. +32 for every token (q/k RMSNorm, RoPE and the K/V cache write
+  // happen in the attention phase, which holds whole heads)
+  constexpr int ROWS = 16 << LNR_QKV;
   const int M = a.M;
-  const int64_t* lp = a.layers + (size_t)layer * NFIELD;
-  const bf16* qn = (const bf16*)lp[F_QN];
-  const bf16* kn = (const bf16*)lp[F_KN];
-  bf16* kc = (bf16*)lp[F_KC];
-  bf16* vc = (bf16*)lp[F_VC];
   const int t = tid();
-  const int m = t >> 5, j = t & 31;        // token m, dims {j, j+32, j+64, j+96}
-  const bool act = m < M;
-  int64_t p = act ? a.pos[m] : 0;
-  const bool pok = p >= 0 && p < a.cap && p < a.rope_rows;
-  if (act && !pok && j == 0) atomicOr(a.err, E_POS);
-  float x[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) x[q] = act ? rbf(res[j + 32 * q][m]) : 0.f;
-  const int NKV = a.NKV, NH = a.NH;
-  if (head >= NH + NKV) {
-    if (act && pok) {
-      const rsrc_t vr = make_rsrc(vc, (unsigned)((size_t)M * NKV * a.cap * HD * 2));
-      const size_t base = (((size_t)m * NKV + (head - NH - NKV)) * a.cap + p) * HD;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) stc_b16(vr, (unsigned)((base + j + 32 * q) * 2), f2bf(x[q]));
-    }
-    return;
-  }
-  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);   // 32 lanes of token m
-  const float r = rsqrt_ieee(ss / (float)HD + a.eps);
-  const bf16* wn = head < NH ? qn : kn;
-  float n[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) n[q] = rbf(rbf(x[q] * r) * bf2f(wn[j + 32 * q]));
-  if (!act || !pok) return;
-  // rotate-half pairs: (j, j+64) and (j+32, j+96)
-  const size_t cb = (size_t)p * HD;
-  float o4[4];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int d = j + 32 * q;                  // d < 64, partner d + 64
-    const float c1 = bf2f(a.cos_t[cb + d]), c2 = bf2f(a.cos_t[cb + d + 64]);
-    const float s1 = bf2f(a.sin_t[cb + d]), s2 = bf2f(a.sin_t[cb + d + 64]);
-    o4[q] = rbf(rbf(n[q] * c1) + rbf(-n[q + 2] * s1));
-    o4[q + 2] = rbf(rbf(n[q + 2] * c2) + rbf(n[q] * s2));
-  }
-  if (head < NH) {
-    const rsrc_t qr = make_rsrc(q_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
-    const size_t base = ((size_t)m * NH + head) * HD;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) stc_b16(qr, (unsigned)((base + j + 32 * q) * 2), f2bf(o4[q]));
-  } else {
-    const rsrc_t kr = make_rsrc(kc, (unsigned)((size_t)M * NKV * a.cap * HD * 2));
-    const size_t base = (((size_t)m * NKV + (head - NH)) * a.cap + p) * HD;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) stc_b16(kr, (unsigned)((base + j + 32 * q) * 2), f2bf(o4[q]));
+  const int r = t % ROWS, m = t / ROWS;
+  const int nqkv = (a.NH + 2 * a.NKV) * HD;
+  if (m < M) {
+    const rsrc_t qr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
+    stc_b16(qr, (unsigned)((size_t)m * nqkv + grp * ROWS + r) * 2, f2bf(res[r][m]));
   }
 }
 
@@ -476,8 +457,20 @@ __device__ __forceinline__ void epi_logits(const Args& a, Shared& sh, float (*re
   }
 }
 
-// Reduce the waves' tiles of one row group, finish the group (directly, or through partials
-// when it is shared with other workgroups) and run the epilogue.
+// Run the epilogue of a row group whose fp32 sums are in res.
+template <int EPI>
+__device__ __forceinline__ void run_epilogue(const Args& a, Shared& sh, float (*res)[MAXM + 1],
+                                             int grp, int layer) {
+  if (EPI == EPI_QKV) epi_qkv(a, res, layer, grp);
+  else if (EPI == EPI_RES) epi_res(a, res, grp, layer);   // layer: output h slot
+  else if (EPI == EPI_SILU) epi_silu(a, res, grp, layer);
+  else epi_logits(a, sh, res, grp);
+}
+
+// Reduce the waves' tiles of one row group and finish it: directly when this workgroup owns the
+// whole group, else through partials, finished by the last contributor to arrive (partials
+// summed in workgroup order, CB contributors' loads in flight at once; an empty contributor
+// adds +0).
 template <int NR, int EPI>
 __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
                             f32x4 (&acc)[NR]) {
@@ -521,8 +514,6 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
     for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
     finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
     if (finish) {
-      // sum the contributors' partials in workgroup order, CB contributors' loads in flight at
-      // once (an empty contributor adds +0)
       constexpr int EPT = (NR * 16 * MAXM + NTHR - 1) / NTHR;
       constexpr int CB = 4;
       float acc[EPT];
@@ -558,12 +549,7 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
       __syncthreads();
     }
   }
-  if (finish) {
-    if (EPI == EPI_QKV) epi_qkv(a, L.res, layer, grp);
-    else if (EPI == EPI_RES) epi_res(a, L.res, grp, layer);   // layer: output h slot
-    else if (EPI == EPI_SILU) epi_silu(a, L.res, grp, layer);
-    else epi_logits(a, sh, L.res, grp);
-  }
+  if (finish) run_epilogue<EPI>(a, sh, L.res, grp, layer);
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
 }
@@ -660,221 +646,317 @@ __device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo&
 }
 
 // ---------------------------------------------------------------------------------------------
-// attention: units (row b, kv head, chunk of C keys); see attn.hip for the MFMA formulation.
+// attention. The 32-key blocks of every (row, kv head) are laid end to end (row-major, then kv
+// head) and split into equal contiguous workgroup ranges, so every workgroup streams the same
+// number of K/V bytes whatever the per-row context lengths. A workgroup takes its range as
+// segments, one per (row, kv head) it touches; its 8 waves share a segment's blocks.
+// Per segment: the G query heads are RMS-normalised and rotated from the raw q|k|v (engine.py
+// qkv_post), the segment holding the newest block also normalises/rotates k and writes K/V at
+// pos; then S^T = K.Q^T and O^T += V^T.P^T on MFMA (P rounded to bf16), the waves merge through
+// LDS, and a (row, kv head) split over workgroups is combined (log-sum-exp, in workgroup order)
+// by the last contributor to arrive.
+
+// q/k head RMSNorm (weight w) and RoPE at position p for one head held by a wave: lane l holds
+// dims l and l + 64. v (norm == false) passes through.
+__device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& x1, const bf16* w,
+                                               int64_t p, bool rope, int lane) {
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float r = rsqrt_ieee(ss / (float)HD + a.eps);
+  const float n0 = rbf(rbf(x0 * r) * bf2f(w[lane]));
+  const float n1 = rbf(rbf(x1 * r) * bf2f(w[lane + 64]));
+  if (rope) {
+    const size_t cb = (size_t)p * HD;
+    const float c0 = bf2f(a.cos_t[cb + lane]), c1 = bf2f(a.cos_t[cb + lane + 64]);
+    const float s0 = bf2f(a.sin_t[cb + lane]), s1 = bf2f(a.sin_t[cb + lane + 64]);
+    x0 = rbf(rbf(n0 * c0) + rbf(-n1 * s0));
+    x1 = rbf(rbf(n1 * c1) + rbf(n0 * s1));
+  } else {
+    x0 = n0;
+    x1 = n1;
+  }
+}
+
+__device__ __forceinline__ int attn_owner(int T, int i) {          // workgroup of global unit i
+  return (int)((((long long)i + 1) * gridDim.x - 1) / T);
+}
+__device__ __forceinline__ int attn_first(int T, int c) {          // first unit of workgroup c
+  return (int)((long long)T * c / gridDim.x);
+}
+
+// Partition units of one (row, kv head): ATT_OVH units for its fixed per-segment latency
+// (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
+// many short segments gets fewer blocks.
+constexpr int ATT_OVH = 12;
+constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
+
 __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer) {
-  const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV, C = a.chunk;
+  const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
   const int lane = tid() & 63, wave = wave_id();
   const int l16 = lane & 15, g4 = lane >> 4;
   const int64_t* lp = a.layers + (size_t)layer * NFIELD;
-  const bf16* kc = (const bf16*)lp[F_KC];
-  const bf16* vc = (const bf16*)lp[F_VC];
+  bf16* kc = (bf16*)lp[F_KC];
+  bf16* vc = (bf16*)lp[F_VC];
+  const bf16* qnw = (const bf16*)lp[F_QN];
+  const bf16* knw = (const bf16*)lp[F_KN];
+  const int nqkv = (NH + 2 * NKV) * HD;
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
   if (tid() == 0) {
     int acc = 0;
     for (int b = 0; b < M; ++b) {
       sh.units[b] = acc;
       const int64_t p = a.pos[b];
-      const int L = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
-      acc += NKV * ((L + C - 1) / C);
+      if ((p < 0 || p >= a.cap || p >= a.rope_rows) && blockIdx.x == 0) atomicOr(a.err, E_POS);
+      const int Lb = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
+      const int nblk = (Lb + 31) >> 5;
+      acc += nblk > 0 ? NKV * (ATT_OVH + nblk) : 0;
     }
     sh.units[M] = acc;
   }
   __syncthreads();
-  const int U = sh.units[M];
-  const int u0 = (int)((long long)U * blockIdx.x / gridDim.x);
-  const int u1 = (int)((long long)U * (blockIdx.x + 1) / gridDim.x);
-  const size_t kvrow = (size_t)HD;
-  const rsrc_t qr = make_rsrc(q_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
+  const int T = sh.units[M];
+  const int i0 = attn_first(T, blockIdx.x), i1 = attn_first(T, blockIdx.x + 1);
+  const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
+  const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
+  const rsrc_t rawr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
-  const int maxch = (a.cap + C - 1) / C;
-  const unsigned wsrow = HD + 2;
-  const rsrc_t pr = make_rsrc(a.ws + a.off_att, (unsigned)((size_t)MAXM * NKV * maxch * G * wsrow * 4));
-  for (int u = u0; u < u1; ++u) {
-    int b = 0;
-    while (b + 1 < M && sh.units[b + 1] <= u) ++b;
-    const int64_t p0 = a.pos[b];
-    const int L = (int)min<int64_t>(p0 + 1, (int64_t)a.cap);
-    const int nch = (L + C - 1) / C;
-    const int r = u - sh.units[b];
-    const int kvh = r / nch, c = r - (r / nch) * nch;
-    const int start = c * C, end = min(start + C, L);
-    const int bk = b * NKV + kvh;
-    const size_t kvbase = (size_t)bk * a.cap * kvrow;
-    // Q^T operand (rows = the G query heads of this kv head; rows >= G zero)
-    u32x4 qreg[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      qreg[kb] = l16 < G ? ldb128(qr, (unsigned)((((size_t)b * NH + kvh * G + l16) * HD + kb * 32 + g4 * 8) * 2))
-                         : u32x4{0u, 0u, 0u, 0u};
-    f32x4 acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
-    bf16(*vs)[HD + 8] = sh.u.a.v[wave];
-    const int nblk = (end - start + 31) >> 5;
-    for (int bi = wave; bi < nblk; bi += NWAVE) {
-      const int j0 = start + bi * 32;
-      // K/V of this launch's position were written through to the coherence point in this
-      // layer's QKV phase and never read before in this launch: plain loads see them
-      u32x4 kreg[2][4];
-      u32x4 vreg[8];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        int key = j0 + t * 16 + l16;
-        key = key < a.cap ? key : a.cap - 1;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const size_t off = kvbase + (size_t)key * kvrow + kb * 32 + g4 * 8;
-          kreg[t][kb] = ld16(kc + off);
+  const unsigned rec = HD + 2;                                        // o[128], m, l
+  const rsrc_t pr = make_rsrc(a.ws + a.off_att, (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
+  const int maxseg = ATT_QN / G;
+  bool first_seg = true;
+  for (int i = i0; i < i1;) {
+    // ---- this round's segments: (row, kv head) pairs whose blocks meet [i, i1)
+    if (tid() == 0) {
+      int n = 0, u = i;
+      while (u < i1 && n < maxseg) {
+        int b = 0;
+        while (b + 1 < M && sh.units[b + 1] <= u) ++b;
+        const int Lb = (int)min<int64_t>(max<int64_t>(a.pos[b] + 1, 0), (int64_t)a.cap);
+        const int nblk = (Lb + 31) >> 5;
+        const int per = ATT_OVH + nblk;
+        const int kvh = (u - sh.units[b]) / per;
+        const int S = sh.units[b] + kvh * per;                      // pair start (overhead units)
+        const int lo = max(u, S + ATT_OVH), hi = min(i1, S + per);
+        if (hi > lo) {
+          sh.seg[n][0] = b;
+          sh.seg[n][1] = kvh;
+          sh.seg[n][2] = lo - S - ATT_OVH;
+          sh.seg[n][3] = hi - lo;
+          ++n;
         }
+        u = S + per;
       }
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int cc = it * 64 + lane;
-        int key = j0 + (cc >> 4);
-        key = key < a.cap ? key : a.cap - 1;
-        const size_t off = kvbase + (size_t)key * kvrow + (cc & 15) * 8;
-        vreg[it] = ld16(vc + off);
+      sh.nseg = n;
+      sh.segnext = u;                                               // where the next round starts
+    }
+    __syncthreads();
+    const int nsg = sh.nseg;
+    const int inext = sh.segnext;
+    // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; the
+    // segment holding the newest block also writes K/V of position pos
+    for (int task = wave; task < nsg * (G + 2); task += NWAVE) {
+      const int sg = task / (G + 2), tk = task - sg * (G + 2);
+      const int b = sh.seg[sg][0], kvh = sh.seg[sg][1];
+      const int64_t p0 = a.pos[b];
+      const int Lb = (int)min<int64_t>(max<int64_t>(p0 + 1, 0), (int64_t)a.cap);
+      const bool newest = sh.seg[sg][2] + sh.seg[sg][3] == ((Lb + 31) >> 5);
+      const bool pok = p0 >= 0 && p0 < a.cap && p0 < a.rope_rows;
+      if (tk >= G && !(newest && pok)) continue;
+      const int col = tk < G ? (kvh * G + tk) * HD : tk == G ? (NH + kvh) * HD : (NH + NKV + kvh) * HD;
+      const unsigned ro = (unsigned)((size_t)b * nqkv + col) * 2;
+      float x0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rawr, ro + lane * 2, 0, 0));
+      float x1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rawr, ro + (lane + 64) * 2, 0, 0));
+      if (tk <= G) head_norm_rope(a, x0, x1, tk < G ? qnw : knw, p0, pok, lane);
+      if (tk < G) {
+        sh.u.a.qn[sg * G + tk][lane] = f2bf(x0);
+        sh.u.a.qn[sg * G + tk][lane + 64] = f2bf(x1);
+      } else {
+        const rsrc_t cr = tk == G ? kwr : vwr;
+        const unsigned co = (unsigned)(((size_t)(b * NKV + kvh) * a.cap + p0) * HD * 2);
+        stc_b16(cr, co + lane * 2, f2bf(x0));
+        stc_b16(cr, co + (lane + 64) * 2, f2bf(x1));
       }
-      f32x4 sc[2];
+    }
+    __builtin_amdgcn_s_waitcnt(0);          // K/V at pos written through before anyone reads it
+    __syncthreads();
+    for (int sg = 0; sg < nsg; ++sg) {
+      const int b = sh.seg[sg][0], kvh = sh.seg[sg][1], j0 = sh.seg[sg][2], nseg = sh.seg[sg][3];
+      const int64_t p0 = a.pos[b];
+      const int Lb = (int)min<int64_t>(max<int64_t>(p0 + 1, 0), (int64_t)a.cap);
+      const int nblk = (Lb + 31) >> 5;
+      const int bk = b * NKV + kvh;
+      const size_t kvbase = (size_t)bk * a.cap * HD;
+      const int S = sh.units[b] + kvh * (ATT_OVH + nblk);
+      // Q^T operand (rows = the G query heads of this kv head; rows >= G zero)
+      u32x4 qreg[4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 4; ++kb)
+        qreg[kb] = l16 < G ? *(const u32x4*)&sh.u.a.qn[sg * G + l16][kb * 32 + g4 * 8]
+                           : u32x4{0u, 0u, 0u, 0u};
+      f32x4 acc[8];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) d = mfma16x16x32(kreg[t][kb], qreg[kb], d);
-        sc[t] = d;
-      }
+      for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float m_run = -INFINITY, l_run = 0.f;
+      bf16(*vs)[HD + 8] = sh.u.a.v[wave];
+      for (int k = wave; k < nseg; k += NWAVE) {
+        const int key0 = (j0 + k) * 32;
+        u32x4 kreg[2][4];
+        u32x4 vreg[8];
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int cc = it * 64 + lane;
-        *(u32x4*)&vs[cc >> 4][(cc & 15) * 8] = vreg[it];
-      }
-      float sv[8];
-      float mloc = -INFINITY;
+        for (int t = 0; t < 2; ++t) {
+          int key = key0 + t * 16 + l16;
+          key = key < a.cap ? key : a.cap - 1;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = j0 + t * 16 + g4 * 4 + i;
-          const float v = key < end ? sc[t][i] * scale_log2 : -INFINITY;
-          sv[t * 4 + i] = v;
-          mloc = fmaxf(mloc, v);
+          for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
         }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run, mloc);
-      const float msafe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - msafe);
-      float psum = 0.f;
-      unsigned pk[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float pa = exp2f(sv[2 * jj] - msafe);
-        const float pb = exp2f(sv[2 * jj + 1] - msafe);
-        psum += pa + pb;
-        pk[jj] = (unsigned)f2bf(pa) | ((unsigned)f2bf(pb) << 16);
-      }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+        for (int it = 0; it < 8; ++it) {
+          const int cc = it * 64 + lane;
+          int key = key0 + (cc >> 4);
+          key = key < a.cap ? key : a.cap - 1;
+          vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
+        }
+        f32x4 sc[2];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-      const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int t = 0; t < 2; ++t) {
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = dt * 16 + l16;
-        unsigned av[4];
+          for (int kb = 0; kb < 4; ++kb) d = mfma16x16x32(kreg[t][kb], qreg[kb], d);
+          sc[t] = d;
+        }
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const int cc = it * 64 + lane;
+          *(u32x4*)&vs[cc >> 4][(cc & 15) * 8] = vreg[it];
+        }
+        float sv[8];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int key = key0 + t * 16 + g4 * 4 + q;
+            const float v = key < Lb ? sc[t][q] * scale_log2 : -INFINITY;
+            sv[t * 4 + q] = v;
+            mloc = fmaxf(mloc, v);
+          }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float msafe = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m_run - msafe);
+        float psum = 0.f;
+        unsigned pk[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int ka = (jj < 2) ? (g4 * 4 + 2 * jj) : (16 + g4 * 4 + 2 * (jj - 2));
-          av[jj] = (unsigned)vs[ka][d] | ((unsigned)vs[ka + 1][d] << 16);
+          const float pa = exp2f(sv[2 * jj] - msafe);
+          const float pb = exp2f(sv[2 * jj + 1] - msafe);
+          psum += pa + pb;
+          pk[jj] = pk_bf16(pa, pb);
         }
-        acc[dt] = mfma16x16x32(u32x4{av[0], av[1], av[2], av[3]}, pB, acc[dt]);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    // merge the waves (rows < G)
-    __syncthreads();
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sh.u.a.mrg[wave][l16][dt * 16 + g4 * 4 + i] = acc[dt][i];
-    if (g4 == 0) {
-      sh.ms[wave][l16] = m_run;
-      sh.ls[wave][l16] = l_run;
-    }
-    __syncthreads();
-    for (int e = tid(); e < G * HD; e += NTHR) {
-      const int row = e / HD, d = e % HD;
-      float Mx = -INFINITY;
+        for (int dt = 0; dt < 8; ++dt) {
+          const int d = dt * 16 + l16;
+          unsigned av[4];
 #pragma unroll
-      for (int w = 0; w < NWAVE; ++w) Mx = fmaxf(Mx, sh.ms[w][row]);
-      const float Ms = Mx == -INFINITY ? 0.f : Mx;
-      float o = 0.f, l = 0.f;
-#pragma unroll
-      for (int w = 0; w < NWAVE; ++w) {
-        const float f = exp2f(sh.ms[w][row] - Ms);
-        o += sh.u.a.mrg[w][row][d] * f;
-        l += sh.ls[w][row] * f;
-      }
-      const unsigned oidx = (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2;
-      if (nch == 1) {
-        stc_b16(orr, oidx, f2bf(o / l));
-      } else {
-        const unsigned pb = (unsigned)((((size_t)bk * maxch + c) * G + row) * wsrow) * 4;
-        stc_f32(pr, pb + d * 4, o);
-        if (d == 0) {
-          stc_f32(pr, pb + HD * 4, Mx);
-          stc_f32(pr, pb + (HD + 1) * 4, l);
+          for (int jj = 0; jj < 4; ++jj) {
+            const int ka = (jj < 2) ? (g4 * 4 + 2 * jj) : (16 + g4 * 4 + 2 * (jj - 2));
+            av[jj] = (unsigned)vs[ka][d] | ((unsigned)vs[ka + 1][d] << 16);
+          }
+          acc[dt] = mfma16x16x32(u32x4{av[0], av[1], av[2], av[3]}, pB, acc[dt]);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-    }
-    if (nch > 1 && arrive_last(a.ctr + C_ATT + bk, nch, &sh.flag)) {
-      // log-sum-exp combine of the chunks, QB chunks' loads in flight at once
-      constexpr int QB = 8;
+      // merge the waves (rows < G)
+      __syncthreads();
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sh.u.a.mrg[wave][l16][dt * 16 + g4 * 4 + q] = acc[dt][q];
+      if (g4 == 0) {
+        sh.ms[wave][l16] = m_run;
+        sh.ls[wave][l16] = l_run;
+      }
+      __syncthreads();
+      const bool whole = j0 == 0 && nseg == nblk;
+      const int myslot = first_seg ? 0 : 1;
+      first_seg = false;
       for (int e = tid(); e < G * HD; e += NTHR) {
         const int row = e / HD, d = e % HD;
-        const unsigned pb0 = (unsigned)((((size_t)bk * maxch) * G + row) * wsrow) * 4;
-        const unsigned cs = (unsigned)(G * wsrow) * 4;
         float Mx = -INFINITY;
-        for (int q0 = 0; q0 < nch; q0 += QB) {
-          float mv[QB];
 #pragma unroll
-          for (int j = 0; j < QB; ++j)
-            mv[j] = q0 + j < nch ? ldc_f32(pr, pb0 + (q0 + j) * cs + HD * 4) : -INFINITY;
-#pragma unroll
-          for (int j = 0; j < QB; ++j) Mx = fmaxf(Mx, mv[j]);
-        }
+        for (int w = 0; w < NWAVE; ++w) Mx = fmaxf(Mx, sh.ms[w][row]);
+        const float Ms = Mx == -INFINITY ? 0.f : Mx;
         float o = 0.f, l = 0.f;
-        for (int q0 = 0; q0 < nch; q0 += QB) {
-          float mv[QB], ov[QB], lv[QB];
 #pragma unroll
-          for (int j = 0; j < QB; ++j) {
-            const bool ok = q0 + j < nch;
-            const unsigned qb = pb0 + (q0 + j) * cs;
-            mv[j] = ok ? ldc_f32(pr, qb + HD * 4) : -INFINITY;
-            ov[j] = ok ? ldc_f32(pr, qb + d * 4) : 0.f;
-            lv[j] = ok ? ldc_f32(pr, qb + (HD + 1) * 4) : 0.f;
-          }
-#pragma unroll
-          for (int j = 0; j < QB; ++j) {
-            if (q0 + j < nch) {
-              const float f = exp2f(mv[j] - Mx);
-              o += ov[j] * f;
-              l += lv[j] * f;
-            }
+        for (int w = 0; w < NWAVE; ++w) {
+          const float f = exp2f(sh.ms[w][row] - Ms);
+          o += sh.u.a.mrg[w][row][d] * f;
+          l += sh.ls[w][row] * f;
+        }
+        if (whole) {
+          stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
+        } else {
+          const unsigned pb = (unsigned)(((blockIdx.x * 2 + myslot) * G + row) * rec) * 4;
+          stc_f32(pr, pb + d * 4, o);
+          if (d == 0) {
+            stc_f32(pr, pb + HD * 4, Mx);
+            stc_f32(pr, pb + (HD + 1) * 4, l);
           }
         }
-        stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
       }
+      if (!whole) {
+        // contributors: the workgroups fw..lw holding blocks of (b, kvh), in order; for each,
+        // (b, kvh) is its first segment exactly when its range starts inside the pair's units
+        const int fw = attn_owner(T, S + ATT_OVH), lw = attn_owner(T, S + ATT_OVH + nblk - 1);
+        int ncontrib = 0;
+        for (int c = fw; c <= lw; ++c) ncontrib += attn_first(T, c + 1) > attn_first(T, c);
+        if (arrive_last(a.ctr + C_ATT + bk, ncontrib, &sh.flag)) {
+          constexpr int QB = 4;
+          for (int e = tid(); e < G * HD; e += NTHR) {
+            const int row = e / HD, d = e % HD;
+            float mv[QB], ov[QB], lv[QB];
+            float Mx = -INFINITY, o = 0.f, l = 0.f;
+            for (int c0 = fw; c0 <= lw; c0 += QB) {
+#pragma unroll
+              for (int q = 0; q < QB; ++q) {
+                const int c = c0 + q;
+                const int cb0 = attn_first(T, c);
+                const bool ok = c <= lw && attn_first(T, c + 1) > cb0;
+                const unsigned qb = (unsigned)(((c * 2 + (cb0 >= S ? 0 : 1)) * G + row) * rec) * 4;
+                mv[q] = ok ? ldc_f32(pr, qb + HD * 4) : -INFINITY;
+                ov[q] = ok ? ldc_f32(pr, qb + d * 4) : 0.f;
+                lv[q] = ok ? ldc_f32(pr, qb + (HD + 1) * 4) : 0.f;
+              }
+              // online in workgroup order: rescale the running sums when the max grows
+#pragma unroll
+              for (int q = 0; q < QB; ++q) {
+                if (mv[q] == -INFINITY) continue;
+                const float Mn = fmaxf(Mx, mv[q]);
+                const float fo = exp2f(Mx - Mn), fn = exp2f(mv[q] - Mn);
+                o = o * fo + ov[q] * fn;
+                l = l * fo + lv[q] * fn;
+                Mx = Mn;
+              }
+            }
+            stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
+          }
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
+    i = inext;
   }
 }
 
@@ -922,11 +1004,11 @@ __device__ __forceinline__ bool phase_geo(const Args& a, int p, Geo* g) {
   const int kind = phase_kind(a, p, &layer);
   const int64_t* lp = layer >= 0 ? a.layers + (size_t)layer * NFIELD : nullptr;
   switch (kind) {
-    case P_QKV: *g = make_geo((const bf16*)lp[F_WQKV], (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV); return true;
-    case P_O:   *g = make_geo((const bf16*)lp[F_WO], a.H, a.NH * HD, LNR_O); return true;
-    case P_GU:  *g = make_geo((const bf16*)lp[F_WGU], 2 * a.I, a.H, LNR_GU); return true;
-    case P_D:   *g = make_geo((const bf16*)lp[F_WD], a.H, a.I, LNR_D); return true;
-    case P_LM:  *g = make_geo(a.lm_t, a.V, a.H, LNR_LM); return true;
+    case P_QKV: *g = make_geo((const bf16*)lp[F_WQKV], (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV, true); return true;
+    case P_O:   *g = make_geo((const bf16*)lp[F_WO], a.H, a.NH * HD, LNR_O, false); return true;
+    case P_GU:  *g = make_geo((const bf16*)lp[F_WGU], 2 * a.I, a.H, LNR_GU, false); return true;
+    case P_D:   *g = make_geo((const bf16*)lp[F_WD], a.H, a.I, LNR_D, false); return true;
+    case P_LM:  *g = make_geo(a.lm_t, a.V, a.H, LNR_LM, true); return true;
     default: return false;
   }
 }
@@ -945,7 +1027,7 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g
   issue_batch<NR>(g, BATCH / NR, B);
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
-  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss);
+  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss, p);
   STEP_TRACE(p, 2);
   gemv_phase<NR, EPI>(a, sh, g, layer, A, B);
   STEP_TRACE(p, 3);
@@ -1105,13 +1187,12 @@ static int step_grid(int* G_out) {
 
 struct WsLayout { size_t ss, part, att, am, total; };
 
-static WsLayout ws_layout(int L, int G, int NKV, int G_heads, int cap, int chunk) {
+static WsLayout ws_layout(int L, int G, int G_heads) {
   WsLayout w;
   w.ss = 0;
   w.part = (size_t)(2 * L + 1) * SS_SLOT;                   // ss: [2L+1][H/64 <= 64][16]
-  w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // 2 slots of <= 128 rows x 16
-  const size_t maxch = (size_t)(cap + chunk - 1) / chunk;
-  w.am = w.att + (size_t)MAXM * NKV * maxch * G_heads * (HD + 2);
+  w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // GEMV: 2 slots of <= 128 rows x 16
+  w.am = w.att + (size_t)G * 2 * G_heads * (HD + 2);        // attention: 2 slots of G heads
   w.total = w.am + (size_t)G * MAXM * 2;
   return w;
 }
@@ -1123,10 +1204,15 @@ DD_API int dd_step_grid(void) {
 
 DD_API int dd_step_counters(void) { return C_TOTAL; }
 
-DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV, int cap, int chunk) {
+DD_API int dd_step_nr(int matrix) {
+  const int lnr[5] = {LNR_QKV, LNR_O, LNR_GU, LNR_D, LNR_LM};
+  return matrix >= 0 && matrix < 5 ? 1 << lnr[matrix] : 0;
+}
+
+DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV) {
   int G = 0;
-  if (L < 1 || NKV < 1 || NH < NKV || cap < 1 || chunk < 32 || step_grid(&G) != 0) return 0;
-  return ws_layout(L, G, NKV, NH / NKV, cap, chunk).total * sizeof(float);
+  if (L < 1 || NKV < 1 || NH < NKV || step_grid(&G) != 0) return 0;
+  return ws_layout(L, G, NH / NKV).total * sizeof(float);
 }
 
 DD_API size_t dd_tiled_bytes(int N, int K) { return (size_t)N * K * 2; }
@@ -1155,6 +1241,7 @@ static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int 
   const int K_of[5] = {H, NH * HD, H, I, H};
   const int rows_of[5] = {(NH + 2 * NKV) * HD, H, 2 * I, H, V};
   const int lnr_of[5] = {LNR_QKV, LNR_O, LNR_GU, LNR_D, LNR_LM};
+  const bool whole_of[5] = {true, false, false, false, true};   // as in phase_geo
   for (int q = 0; q < 5; ++q) {
     const int K = K_of[q], rows = rows_of[q], lnr = lnr_of[q];
     if (K % 32 != 0 || rows % (16 << lnr) != 0) return false;
@@ -1164,7 +1251,7 @@ static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int 
     if (G > 0) {
       const long long S = (long long)(rows >> (4 + lnr)) * nk;
       const long long per = (S + G - 1) / G;
-      const long long nw = per < nk ? per : nk;
+      const long long nw = whole_of[q] || per > nk ? nk : per;
       if ((nw * 64 + 16) * M > (long long)x_capacity(1 << lnr)) return false;
     }
   }
@@ -1179,20 +1266,20 @@ DD_API int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M)
 
 DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,
                           const void* final_norm, const void* cos_t, const void* sin_t,
-                          int rope_rows, int64_t* tok, int64_t* pos, void* h, void* qbuf,
+                          int rope_rows, int64_t* tok, int64_t* pos, void* h, void* qkv,
                           void* attn, void* mbuf, void* logits, void* ws, int* counters, int* err,
                           int M, int H, int NH, int NKV, int I, int V, int cap, float eps,
-                          int chunk, int phase_begin, int phase_end, hipStream_t stream) {
+                          int phase_begin, int phase_end, hipStream_t stream) {
   DD_REQUIRE(layer_table && embed && lm_tiled && final_norm && cos_t && sin_t && tok && pos);
-  DD_REQUIRE(h && qbuf && attn && mbuf && logits && ws && counters && err);
+  DD_REQUIRE(h && qkv && attn && mbuf && logits && ws && counters && err);
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, 0));
-  DD_REQUIRE(chunk >= 32 && chunk % 32 == 0 && cap >= 1 && rope_rows >= 1);
+  DD_REQUIRE(cap >= 1 && rope_rows >= 1);
   DD_REQUIRE(phase_begin >= 0 && phase_begin < phase_end && phase_end <= 2 + 5 * L);
   int G = 0;
   const int e = step_grid(&G);
   if (e != 0) return e;
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, G));
-  const WsLayout w = ws_layout(L, G, NKV, NH / NKV, cap, chunk);
+  const WsLayout w = ws_layout(L, G, NH / NKV);
   Args a;
   a.layers = layer_table;
   a.embed = (const bf16*)embed;
@@ -1203,7 +1290,7 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   a.tok = tok;
   a.pos = pos;
   a.h = (bf16*)h;
-  a.qbuf = (bf16*)qbuf;
+  a.qkv = (bf16*)qkv;
   a.attn = (bf16*)attn;
   a.mbuf = (bf16*)mbuf;
   a.logits = (bf16*)logits;
@@ -1211,7 +1298,7 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   a.ctr = counters;
   a.err = err;
   a.L = L; a.M = M; a.H = H; a.NH = NH; a.NKV = NKV; a.I = I; a.V = V;
-  a.cap = cap; a.rope_rows = rope_rows; a.chunk = chunk; a.eps = eps;
+  a.cap = cap; a.rope_rows = rope_rows; a.eps = eps;
   a.phase_begin = phase_begin;
   a.phase_end = phase_end;
   a.off_ss = (unsigned)w.ss;

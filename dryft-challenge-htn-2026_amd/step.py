@@ -22,9 +22,6 @@ from ._lib import check, lib
 MAXM = 16
 HD = 128
 NFIELD = 16
-# tiles per row group (the kernel's compile-time layout): wqkv, wo, wgu, wd, lm_head
-NR_QKV, NR_O, NR_GU, NR_D, NR_LM = 8, 4, 2, 4, 2
-CHUNK = 256           # keys per attention split
 
 
 def _stream(dev):
@@ -47,13 +44,15 @@ class FusedStep:
         self.I = e.layers[0].wd.shape[1]
         if not self.L.dd_step_supported(e.L, self.H, e.nh, e.nkv, self.I, self.V, MAXM):
             raise RuntimeError("dd_step_supported: model geometry not taken by the fused step")
+        # tiles per row group of wqkv, wo, wgu, wd, lm_head: the kernel's compile-time layout
+        nr = [self.L.dd_step_nr(i) for i in range(5)]
         with torch.no_grad():
             for l in e.layers:
-                l.wqkv_t = self._tile(l.wqkv, NR_QKV)
-                l.wo_t = self._tile(l.wo, NR_O)
-                l.wgu_t = self._tile(l.wgu, NR_GU, gate_up_I=self.I)
-                l.wd_t = self._tile(l.wd, NR_D)
-            self.lm_t = self._tile(e.lm_head, NR_LM)
+                l.wqkv_t = self._tile(l.wqkv, nr[0])
+                l.wo_t = self._tile(l.wo, nr[1])
+                l.wgu_t = self._tile(l.wgu, nr[2], gate_up_I=self.I)
+                l.wd_t = self._tile(l.wd, nr[3])
+            self.lm_t = self._tile(e.lm_head, nr[4])
         torch.cuda.synchronize(e.dev)
 
     def _tile(self, w, nr, gate_up_I=0):
@@ -78,11 +77,11 @@ class FusedStep:
         # write-once activation slots (see dd_decode_step): h per producing phase, the others
         # per layer
         f.h = torch.empty(2 * L + 1, B, H, **bf)
-        f.qbuf = torch.empty(L, B, e.nh * HD, **bf)
+        f.qkv = torch.empty(L, B, (e.nh + 2 * e.nkv) * HD, **bf)
         f.attn = torch.empty(L, B, e.nh * HD, **bf)
         f.mbuf = torch.empty(L, B, I, **bf)
         f.logits = torch.empty(B, V, **bf)
-        ws = self.L.dd_step_ws_bytes(L, e.nh, e.nkv, st.cap, CHUNK)
+        ws = self.L.dd_step_ws_bytes(L, e.nh, e.nkv)
         if ws == 0:
             raise RuntimeError("dd_step_ws_bytes rejected the shape")
         f.ws = torch.empty(ws // 4, dtype=torch.float32, device=dev)
@@ -106,10 +105,10 @@ class FusedStep:
         check(self.L.dd_decode_step(
             f.table.data_ptr(), e.L, e.embed.data_ptr(), self.lm_t.data_ptr(), e.norm.data_ptr(),
             e.cos.data_ptr(), e.sin.data_ptr(), e.cos.shape[0], st.tok.data_ptr(),
-            st.pos.data_ptr(), f.h.data_ptr(), f.qbuf.data_ptr(), f.attn.data_ptr(),
+            st.pos.data_ptr(), f.h.data_ptr(), f.qkv.data_ptr(), f.attn.data_ptr(),
             f.mbuf.data_ptr(), f.logits.data_ptr(), f.ws.data_ptr(), f.counters.data_ptr(),
             f.err.data_ptr(), st.B, self.H, e.nh, e.nkv, self.I, self.V, st.cap,
-            ctypes.c_float(e.eps), CHUNK, phase_begin, phase_end, _stream(e.dev)),
+            ctypes.c_float(e.eps), phase_begin, phase_end, _stream(e.dev)),
             "dd_decode_step")
         return f.logits
 

@@ -133,15 +133,18 @@ size_t dd_argmax_ws_bytes(int M, int V);
  * matrices stay the interface): block (row group g, k-step s, tile t) = the 16 x 32 bf16
  * MFMA A-operand of rows (g*nr + t)*16 .. +16, columns s*32 .. +32, 1 KB in lane order
  * (lane l: row l%16, columns (l/16)*8 .. +8). gate_up_I > 0 (nr = 2) interleaves gate and up:
- * tile 0 = gate rows g*16.., tile 1 = up rows gate_up_I + g*16... nr per matrix: wqkv 8,
- * wo 4, wgu 2 (gate_up_I = I), wd 4, lm_head 2. dst holds dd_tiled_bytes(N, K). */
+ * tile 0 = gate rows g*16.., tile 1 = up rows gate_up_I + g*16... The nr of each matrix is
+ * dd_step_nr(matrix). dst holds dd_tiled_bytes(N, K). */
 int dd_step_grid(void);
 /* 1 when dd_decode_step takes this model geometry for up to M rows on the current device
  * (head_dim 128; per GEMV phase at least 8 wave-batches of 32-column steps per row group:
  * hidden >= 1024, heads * 128 >= 512, intermediate >= 512; vocab % 32 == 0), else 0. */
 int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M);
 int dd_step_counters(void);
-size_t dd_step_ws_bytes(int L, int NH, int NKV, int cap, int chunk);
+/* Tiles per row group (the nr to pass to dd_tile_weight) of each matrix the step streams:
+ * 0 wqkv, 1 wo, 2 wgu (with gate_up_I = I), 3 wd, 4 lm_head; 0 for any other index. */
+int dd_step_nr(int matrix);
+size_t dd_step_ws_bytes(int L, int NH, int NKV);
 size_t dd_tiled_bytes(int N, int K);
 int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
                    hipStream_t stream);
@@ -152,17 +155,16 @@ int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up
  * tok/pos: [M] int64 (in: this step's tokens and positions; out: the argmax tokens, pos + 1).
  * Activation buffers (bf16), written once per launch (one slot per producing phase, so they
  * are read with plain cached loads): h [2L+1, M, H] (slot 0 embedding, 2l+1 after layer l's
- * O projection, 2l+2 after its down projection), qbuf [L, M, NH, 128], attn [L, M, NH*128],
- * mbuf [L, M, I]; logits [M, V] hold the step's lm_head output afterwards. ws:
- * dd_step_ws_bytes; counters: dd_step_counters() zeroed ints. chunk: keys per attention split
- * (multiple of 32).
+ * O projection, 2l+2 after its down projection), qkv [L, M, (NH + 2 NKV) * 128] (raw q|k|v
+ * projection), attn [L, M, NH*128], mbuf [L, M, I]; logits [M, V] hold the step's lm_head
+ * output afterwards. ws: dd_step_ws_bytes; counters: dd_step_counters() zeroed ints.
  * phase_begin/phase_end select a sub-range of the 2 + 5L phases (0 embedding, 1 + 5l + {0 QKV,
  * 1 attention, 2 O, 3 gate/up, 4 down}, 1 + 5L lm_head/argmax); a full step is 0 .. 2 + 5L. */
 int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,
                    const void* final_norm, const void* cos_t, const void* sin_t, int rope_rows,
-                   int64_t* tok, int64_t* pos, void* h, void* qbuf, void* attn, void* mbuf,
+                   int64_t* tok, int64_t* pos, void* h, void* qkv, void* attn, void* mbuf,
                    void* logits, void* ws, int* counters, int* err, int M, int H, int NH, int NKV,
-                   int I, int V, int cap, float eps, int chunk, int phase_begin, int phase_end,
+                   int I, int V, int cap, float eps, int phase_begin, int phase_end,
                    hipStream_t stream);
 
 /* Measurement helper, no counterpart in the reference: streams `bytes` from p (16-byte words,

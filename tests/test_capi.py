@@ -60,16 +60,16 @@ def test_validation_rejects_without_launch():
 def _step_args(**kw):
     fake = ctypes.c_void_p(0x1000)
     a = dict(layer_table=fake, L=36, embed=fake, lm_tiled=fake, final_norm=fake, cos_t=fake,
-             sin_t=fake, rope_rows=4096, tok=fake, pos=fake, h=fake, qbuf=fake, attn=fake,
+             sin_t=fake, rope_rows=4096, tok=fake, pos=fake, h=fake, qkv=fake, attn=fake,
              mbuf=fake, logits=fake, ws=fake, counters=fake, err=fake, M=16, H=2560, NH=32,
-             NKV=8, I=9728, V=151936, cap=3072, eps=1e-6, chunk=256, phase_begin=0,
+             NKV=8, I=9728, V=151936, cap=3072, eps=1e-6, phase_begin=0,
              phase_end=2 + 5 * 36, stream=None)
     a.update(kw)
     return list(a.values())
 
 
 @pytest.mark.parametrize("bad", [
-    dict(M=17), dict(M=0), dict(NH=30), dict(chunk=100), dict(chunk=16), dict(H=2500),
+    dict(M=17), dict(M=0), dict(NH=30), dict(cap=0), dict(rope_rows=0), dict(H=2500),
     dict(V=151930), dict(phase_end=3 + 5 * 36), dict(phase_begin=5, phase_end=5),
     dict(tok=None), dict(counters=None), dict(NKV=64, NH=64),
 ])
@@ -98,6 +98,7 @@ def test_host_side_sizing():
     assert L.dd_argmax_ws_bytes(16, 151936) == 16 * 38 * 2 * 4
     assert L.dd_tiled_bytes(6144, 2560) == 6144 * 2560 * 2
     assert L.dd_step_counters() >= 1024 + 8192
+    assert [L.dd_step_nr(i) for i in range(6)] == [2, 4, 2, 4, 2, 0]
     # attention: chunk multiple of 128, workspace covers every split of every row
     for B, cap in ((1, 640), (16, 3072), (16, 8192)):
         c = L.dd_attn_chunk(B, 8, cap)

@@ -172,37 +172,46 @@ def _close(got, want, what, rtol=2e-2, atol=2e-2):
     assert not bad.any(), (what, int(bad.sum()), d.max().item())
 
 
+@pytest.mark.parametrize("shape", ["qwen3", "small"])
 @torch.inference_mode()
-def test_fused_phases_per_kernel(cuda):
+def test_fused_phases_per_kernel(cuda, shape):
     """Each phase of the one-launch step run on its own (phase_begin/phase_end) from the buffers
-    the previous phase left, against the oracle's op on exactly those inputs (Qwen3-4B widths,
-    one layer, B=16 ragged positions): per-kernel bf16 tolerance 2e-2, the embedding gather
-    bit-exact, K/V written exactly at pos."""
-    cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
+    the previous phase left, against the oracle's op on exactly those inputs (one layer, B=16
+    ragged positions; Qwen3-4B widths and the small geometry): per-kernel bf16 tolerance 2e-2,
+    the embedding gather bit-exact, K/V written exactly at pos."""
+    if shape == "qwen3":
+        cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
+    else:
+        cfg = dict(SMALL, num_hidden_layers=1)
+    V = cfg["vocab_size"]
     ref, eng = _engine(cfg, seed=12)
     ops, l, rl = ref.ops, eng.layers[0], ref.layers[0]
     g = torch.Generator().manual_seed(13)
     B = 16
     lens = torch.randint(1, 300, (B,), generator=g).tolist()
-    prompts = [torch.randint(0, 8192, (L,), generator=g).tolist() for L in lens]
+    prompts = [torch.randint(0, V, (L,), generator=g).tolist() for L in lens]
     st = eng._new_state(B, 384)
     eng._prefill(prompts, st)
     f = st.fused
-    tok = torch.randint(0, 8192, (B,), generator=g)
+    tok = torch.randint(0, V, (B,), generator=g)
     st.tok.copy_(tok.cuda())
     pos = st.pos.cpu().clone()
     kc0, vc0 = st.kc[0].cpu(), st.vc[0].cpu()
     cpu = lambda t: t.cpu()
 
     # the step's activation buffers are write-once slots: h[0] embedding, h[1] after O, h[2]
-    # after down; q, attention output and SiLU output one slot per layer
-    eng.step.run(st, 0, 2)                                   # embedding + QKV
+    # after down; raw q|k|v, attention output and SiLU output one slot per layer
+    eng.step.run(st, 0, 2)                                   # embedding + QKV projection
     h = cpu(f.h[0])
     assert torch.equal(h.view(torch.int16), ref.embed[tok].view(torch.int16))
-    rkc, rvc = kc0.clone(), vc0.clone()
     qkv = ops.linear(ops.rms(h, rl.ln1), rl.wqkv)
-    q = ops.qkv_post_rows(qkv, rl, rkc, rvc, pos)            # [B, nh, 1, hd]
-    _close(cpu(f.qbuf[0]).view(B, eng.nh, 128), q.reshape(B, eng.nh, 128), "q (norm + rope)")
+    _close(cpu(f.qkv[0]), qkv, "qkv projection")
+    assert torch.equal(st.kc[0].cpu(), kc0) and torch.equal(st.vc[0].cpu(), vc0)
+
+    # attention: q/k RMSNorm + RoPE, K/V written at pos, attention over 0..pos
+    eng.step.run(st, 2, 3)
+    rkc, rvc = kc0.clone(), vc0.clone()
+    q = ops.qkv_post_rows(cpu(f.qkv[0]), rl, rkc, rvc, pos)  # [B, nh, 1, hd], writes rkc/rvc
     for name, c, c0, rc in (("K", st.kc[0], kc0, rkc), ("V", st.vc[0], vc0, rvc)):
         c = c.cpu()
         changed = (c != c0).any(-1).any(1)
@@ -210,11 +219,8 @@ def test_fused_phases_per_kernel(cuda):
             p = int(pos[b])
             assert not changed[b, :p].any() and not changed[b, p + 1:].any(), (name, b)
         idx = pos.view(B, 1, 1, 1).expand(B, eng.nkv, 1, 128)
-        _close(c.gather(2, idx), rc.gather(2, idx), f"{name} write")
-
-    eng.step.run(st, 2, 3)                                   # attention
-    qg = cpu(f.qbuf[0]).view(B, eng.nh, 1, 128)
-    o = ops.attn_decode_rows(qg, st.kc[0].cpu(), st.vc[0].cpu(), pos)
+        _close(c.gather(2, idx), rc.gather(2, idx), f"{name} write (norm + rope)")
+    o = ops.attn_decode_rows(q, st.kc[0].cpu(), st.vc[0].cpu(), pos)
     _close(cpu(f.attn[0]), o, "attention")
 
     attn = cpu(f.attn[0])
