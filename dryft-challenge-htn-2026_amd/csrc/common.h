@@ -116,6 +116,9 @@ __device__ __forceinline__ u32x4 ldc_b128(rsrc_t r, unsigned off) {
 __device__ __forceinline__ void stc_f32(rsrc_t r, unsigned off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, CP_SC1);
 }
+__device__ __forceinline__ void stc_b128(rsrc_t r, unsigned off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, CP_SC1);
+}
 __device__ __forceinline__ void stc_u32(rsrc_t r, unsigned off, unsigned v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, CP_SC1);
 }

@@ -125,15 +125,15 @@ __device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr,
   g.S = g.ngroups * g.nk;
   g.unit = whole ? g.nk : 1;
   g.nu = whole ? g.ngroups : g.S;
-  g.s0 = (int)((long long)g.nu * blockIdx.x / gridDim.x) * g.unit;
-  g.s1 = (int)((long long)g.nu * (blockIdx.x + 1) / gridDim.x) * g.unit;
+  g.s0 = (int)((unsigned)g.nu * blockIdx.x / gridDim.x) * g.unit;
+  g.s1 = (int)((unsigned)g.nu * (blockIdx.x + 1) / gridDim.x) * g.unit;
   g.wr = make_rsrc(W + ((size_t)g.s0 << (9 + lnr)), (unsigned)((g.s1 - g.s0) << (10 + lnr)));
   return g;
 }
 
 // workgroup owning global step s
 __device__ __forceinline__ int wg_of_step(const Geo& g, int s) {
-  return (int)((((long long)(s / g.unit) + 1) * gridDim.x - 1) / g.nu);
+  return (int)(((unsigned)(s / g.unit + 1) * gridDim.x - 1) / (unsigned)g.nu);
 }
 
 // Activation buffers are write-once within a launch: the residual stream h has one slot per
@@ -158,6 +158,10 @@ __device__ __forceinline__ bf16* attn_slot(const Args& a, int l) {
 __device__ __forceinline__ bf16* m_slot(const Args& a, int l) {
   return a.mbuf + (size_t)l * a.M * a.I;
 }
+// split-attention partials of a layer ([G][2][heads per kv head][ATT_REC] fp32): write-once
+__device__ __forceinline__ float* att_part(const Args& a, int l) {
+  return a.ws + a.off_att + (size_t)l * gridDim.x * 2 * (a.NH / a.NKV) * (HD + 4);
+}
 // plain (cached) 16-byte buffer load; out-of-range offsets read zeros
 __device__ __forceinline__ u32x4 ldb128(rsrc_t r, unsigned off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
@@ -165,7 +169,7 @@ __device__ __forceinline__ u32x4 ldb128(rsrc_t r, unsigned off) {
 
 // first step of workgroup c's range (ranges of workgroups between two owners may be empty)
 __device__ __forceinline__ int step0_of(const Geo& g, int c) {
-  return (int)((long long)g.nu * c / gridDim.x) * g.unit;
+  return (int)((unsigned)g.nu * c / gridDim.x) * g.unit;
 }
 
 // Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks). The loads
@@ -194,13 +198,17 @@ constexpr int RES_BYTES = 8 * 16 * (MAXM + 1) * 4;
 __host__ __device__ constexpr int x_capacity(int NR) { return GBUF - NR * NWAVE * 256 * 4 - RES_BYTES; }
 
 constexpr int LNW_KS = 128;                   // k-steps of the norm weight staged in LDS
+constexpr int MAXG = 512;                     // workgroups (CUs) the step kernel supports
+constexpr int MAXG_HEADS = 8;                 // query heads per kv head
+constexpr int MAXL = 64;                      // layers
+constexpr int LFIELDS = 10;                   // layer-table fields the phases read
 
 struct Shared {
   union {
     unsigned char g[GBUF];                    // GEMV phases (see GemvLds)
     struct {                                  // attention
       bf16 v[NWAVE][32][HD + 8];
-      float mrg[NWAVE][16][HD];
+      float mrg[NWAVE][MAXG_HEADS][HD];
       bf16 qn[32][HD];                        // normalised, rotated query heads of the segments
     } a;
   } u;
@@ -217,8 +225,15 @@ struct Shared {
   int units[MAXM + 1];                        // attention unit prefix sums
   int seg[32][4];                             // attention segments: b, kvh, first block, blocks
   int nseg, segnext;
+  long long posv[MAXM];                       // this step's positions (read once at launch)
+  int afirst[MAXG + 1];                       // attention: first unit of each workgroup
+  long long ltab[MAXL][LFIELDS];              // the layer table, copied once per launch
+  int pinfo[MAXM * 32][8];                    // O staging: per (row, kv head) fw, lw, record
+                                              // offsets of its first 3 contributors (-1: none), S
   bf16 lnw[LNW_KS * 32];                      // staged norm weight window (<= LNW_KS k-steps)
 };
+
+static_assert(sizeof(Shared) <= 160 * 1024, "LDS budget of one CU");
 
 // ---------------------------------------------------------------------------------------------
 template <int NR>
@@ -291,24 +306,34 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
     nw = min(g.s1 - g.s0, g.nk);
   }
   const int xrs = nw * 64 + 16;
-  const int items = M * nw * 4;
+  const int W = nw * 4;                       // 16-byte items per row
+  const int items = M * W;
   const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
-  // every workgroup of an XCD may stage the same window: start each one at a different item so
-  // concurrent requests spread over different cache lines
-  const int rot = items > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) % (unsigned)items) : 0;
-  auto item_at = [&](int j) { const int it = j + rot; return it < items ? it : it - items; };
+  // thread t takes items t, t + NTHR, ... (item = m * W + r); (m, r) advance without dividing
+  const int Wd = W > 0 ? W : 1;
+  const int dq = NTHR / Wd, dr = NTHR - dq * Wd;
+  int cm = t / Wd, cr = t - (t / Wd) * Wd;    // the thread's next item
   u32x4 v[SBATCH];
-  auto issue = [&](int base) {
+  int lo_[SBATCH], m_[SBATCH];                // LDS byte offset within the row, row (-1: none)
+  auto issue = [&]() {
 #pragma unroll
     for (int b = 0; b < SBATCH; ++b) {
-      const int j = base + t + b * NTHR;
-      int lds;
-      const unsigned eo = j < items ? stage_off(item_at(j), nw, ksf, g.nk, K, &lds) : 0u;
-      v[b] = ldb128(sr, j < items ? eo * 2 : 0xfffffff0u);
+      const bool ok = cm < M;
+      const int w = cr >> 2, e = cr & 3;
+      int ks = ksf + w;
+      if (ks >= g.nk) ks -= g.nk;
+      lo_[b] = w * 64 + e * 16;
+      m_[b] = ok ? cm : -1;
+      v[b] = ldb128(sr, ok ? (unsigned)((cm * K + ks * 32 + e * 8) * 2) : 0xfffffff0u);
+      cr += dr;
+      cm += dq;
+      if (cr >= Wd) {
+        cr -= Wd;
+        ++cm;
+      }
     }
   };
-  issue(0);
-  STEP_TRACE(p, 4);
+  issue();
   // a norm window beyond the LDS copy (only with fewer workgroups than the window needs) is
   // read from global memory per item instead
   const bool lnw_lds = lnw != nullptr && nw <= LNW_KS;
@@ -341,20 +366,19 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
   }
   __syncthreads();
   for (int base = 0; base < items; base += SBATCH * NTHR) {
-    if (base > 0) issue(base);
+    if (base > 0) issue();
 #pragma unroll
     for (int b = 0; b < SBATCH; ++b) {
-      const int j = base + t + b * NTHR;
-      if (j >= items) break;
-      const int it = item_at(j);
-      int lds;
-      const unsigned eo = stage_off(it, nw, ksf, g.nk, K, &lds);
-      const int m = it / (nw * 4);
+      const int m = m_[b];
+      if (m < 0) break;
       u32x4 x = v[b];
       if (lnw != nullptr) {
         const float r = sh.rs[m];
-        const u32x4 wv = lnw_lds ? *(const u32x4*)&sh.lnw[(lds >> 4) * 8]
-                                 : ld16(lnw + (eo - (unsigned)m * K));
+        const int w = lo_[b] >> 6, e = (lo_[b] >> 4) & 3;
+        int ks = ksf + w;
+        if (ks >= g.nk) ks -= g.nk;
+        const u32x4 wv = lnw_lds ? *(const u32x4*)&sh.lnw[(lo_[b] >> 4) * 8]
+                                 : ld16(lnw + ks * 32 + e * 8);
         const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
         unsigned o[4];
 #pragma unroll
@@ -362,7 +386,7 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
           o[j] = pk_bf16(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]), rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
         x = u32x4{o[0], o[1], o[2], o[3]};
       }
-      *(u32x4*)(xb + m * xrs + lds) = x;
+      *(u32x4*)(xb + m * xrs + lo_[b]) = x;
     }
   }
   STEP_TRACE(p, 6);
@@ -676,51 +700,69 @@ __device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& 
   }
 }
 
+// Partition arithmetic stays in 32 bits (units x workgroups < 2^31, checked on the host).
 __device__ __forceinline__ int attn_owner(int T, int i) {          // workgroup of global unit i
-  return (int)((((long long)i + 1) * gridDim.x - 1) / T);
+  return (int)(((unsigned)(i + 1) * gridDim.x - 1) / (unsigned)T);
 }
 __device__ __forceinline__ int attn_first(int T, int c) {          // first unit of workgroup c
-  return (int)((long long)T * c / gridDim.x);
+  return (int)((unsigned)T * c / gridDim.x);
 }
 
 // Partition units of one (row, kv head): ATT_OVH units for its fixed per-segment latency
 // (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
 // many short segments gets fewer blocks.
 constexpr int ATT_OVH = 12;
+constexpr int ATT_REC = HD + 4;      // split partial record: o[128], m, l, 2 pad (16-byte rows)
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
 
-__device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer) {
+// units[b]: first partition unit of row b (rows with no keys have none); units[M] = total
+__device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool flag_errors) {
+  if (tid() < 64) {                          // wave 0: lane b = row b, prefix sum by shuffles
+    const int b = tid();
+    int cnt = 0;
+    if (b < a.M) {
+      const int64_t p = sh.posv[b];
+      if (flag_errors && (p < 0 || p >= a.cap || p >= a.rope_rows) && blockIdx.x == 0)
+        atomicOr(a.err, E_POS);
+      const int Lb = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
+      const int nblk = (Lb + 31) >> 5;
+      cnt = nblk > 0 ? a.NKV * (ATT_OVH + nblk) : 0;
+    }
+    int inc = cnt;
+#pragma unroll
+    for (int o = 1; o <= MAXM; o <<= 1) {      // lanes 0..MAXM: lane M sums all M rows
+      const int v = __shfl_up(inc, o, 64);
+      if (b >= o) inc += v;
+    }
+    if (b <= a.M) sh.units[b] = inc - cnt;   // lane M: cnt = 0, inc = total
+  }
+  __syncthreads();
+  const int T = sh.units[a.M];
+  for (int c = tid(); c <= (int)gridDim.x; c += NTHR) sh.afirst[c] = attn_first(T, c);
+  __syncthreads();
+}
+
+__device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer, int p) {
   const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
   const int lane = tid() & 63, wave = wave_id();
   const int l16 = lane & 15, g4 = lane >> 4;
-  const int64_t* lp = a.layers + (size_t)layer * NFIELD;
+  const long long* lp = sh.ltab[layer];
   bf16* kc = (bf16*)lp[F_KC];
   bf16* vc = (bf16*)lp[F_VC];
   const bf16* qnw = (const bf16*)lp[F_QN];
   const bf16* knw = (const bf16*)lp[F_KN];
   const int nqkv = (NH + 2 * NKV) * HD;
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
-  if (tid() == 0) {
-    int acc = 0;
-    for (int b = 0; b < M; ++b) {
-      sh.units[b] = acc;
-      const int64_t p = a.pos[b];
-      if ((p < 0 || p >= a.cap || p >= a.rope_rows) && blockIdx.x == 0) atomicOr(a.err, E_POS);
-      const int Lb = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
-      const int nblk = (Lb + 31) >> 5;
-      acc += nblk > 0 ? NKV * (ATT_OVH + nblk) : 0;
-    }
-    sh.units[M] = acc;
-  }
-  __syncthreads();
+  attn_partition(a, sh, true);
+  STEP_TRACE(p, 4);
   const int T = sh.units[M];
   const int i0 = attn_first(T, blockIdx.x), i1 = attn_first(T, blockIdx.x + 1);
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
   const rsrc_t rawr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
-  const unsigned rec = HD + 2;                                        // o[128], m, l
-  const rsrc_t pr = make_rsrc(a.ws + a.off_att, (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
+  const unsigned rec = ATT_REC;
+  const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
   const int maxseg = ATT_QN / G;
   bool first_seg = true;
   for (int i = i0; i < i1;) {
@@ -730,7 +772,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       while (u < i1 && n < maxseg) {
         int b = 0;
         while (b + 1 < M && sh.units[b + 1] <= u) ++b;
-        const int Lb = (int)min<int64_t>(max<int64_t>(a.pos[b] + 1, 0), (int64_t)a.cap);
+        const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
         const int nblk = (Lb + 31) >> 5;
         const int per = ATT_OVH + nblk;
         const int kvh = (u - sh.units[b]) / per;
@@ -756,7 +798,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     for (int task = wave; task < nsg * (G + 2); task += NWAVE) {
       const int sg = task / (G + 2), tk = task - sg * (G + 2);
       const int b = sh.seg[sg][0], kvh = sh.seg[sg][1];
-      const int64_t p0 = a.pos[b];
+      const int64_t p0 = sh.posv[b];
       const int Lb = (int)min<int64_t>(max<int64_t>(p0 + 1, 0), (int64_t)a.cap);
       const bool newest = sh.seg[sg][2] + sh.seg[sg][3] == ((Lb + 31) >> 5);
       const bool pok = p0 >= 0 && p0 < a.cap && p0 < a.rope_rows;
@@ -778,9 +820,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     }
     __builtin_amdgcn_s_waitcnt(0);          // K/V at pos written through before anyone reads it
     __syncthreads();
+    if (first_seg) STEP_TRACE(p, 5);
     for (int sg = 0; sg < nsg; ++sg) {
       const int b = sh.seg[sg][0], kvh = sh.seg[sg][1], j0 = sh.seg[sg][2], nseg = sh.seg[sg][3];
-      const int64_t p0 = a.pos[b];
+      const int64_t p0 = sh.posv[b];
       const int Lb = (int)min<int64_t>(max<int64_t>(p0 + 1, 0), (int64_t)a.cap);
       const int nblk = (Lb + 31) >> 5;
       const int bk = b * NKV + kvh;
@@ -883,12 +926,15 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sh.u.a.mrg[wave][l16][dt * 16 + g4 * 4 + q] = acc[dt][q];
+        for (int q = 0; q < 4; ++q)
+          if (l16 < G) sh.u.a.mrg[wave][l16][dt * 16 + g4 * 4 + q] = acc[dt][q];
       if (g4 == 0) {
         sh.ms[wave][l16] = m_run;
         sh.ls[wave][l16] = l_run;
       }
       __syncthreads();
+      // a (row, kv head) whose blocks all lie in this workgroup is finished here; one split over
+      // workgroups leaves (o, m, l) partials, combined by the O projection's staging
       const bool whole = j0 == 0 && nseg == nblk;
       const int myslot = first_seg ? 0 : 1;
       first_seg = false;
@@ -916,48 +962,11 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
           }
         }
       }
-      if (!whole) {
-        // contributors: the workgroups fw..lw holding blocks of (b, kvh), in order; for each,
-        // (b, kvh) is its first segment exactly when its range starts inside the pair's units
-        const int fw = attn_owner(T, S + ATT_OVH), lw = attn_owner(T, S + ATT_OVH + nblk - 1);
-        int ncontrib = 0;
-        for (int c = fw; c <= lw; ++c) ncontrib += attn_first(T, c + 1) > attn_first(T, c);
-        if (arrive_last(a.ctr + C_ATT + bk, ncontrib, &sh.flag)) {
-          constexpr int QB = 4;
-          for (int e = tid(); e < G * HD; e += NTHR) {
-            const int row = e / HD, d = e % HD;
-            float mv[QB], ov[QB], lv[QB];
-            float Mx = -INFINITY, o = 0.f, l = 0.f;
-            for (int c0 = fw; c0 <= lw; c0 += QB) {
-#pragma unroll
-              for (int q = 0; q < QB; ++q) {
-                const int c = c0 + q;
-                const int cb0 = attn_first(T, c);
-                const bool ok = c <= lw && attn_first(T, c + 1) > cb0;
-                const unsigned qb = (unsigned)(((c * 2 + (cb0 >= S ? 0 : 1)) * G + row) * rec) * 4;
-                mv[q] = ok ? ldc_f32(pr, qb + HD * 4) : -INFINITY;
-                ov[q] = ok ? ldc_f32(pr, qb + d * 4) : 0.f;
-                lv[q] = ok ? ldc_f32(pr, qb + (HD + 1) * 4) : 0.f;
-              }
-              // online in workgroup order: rescale the running sums when the max grows
-#pragma unroll
-              for (int q = 0; q < QB; ++q) {
-                if (mv[q] == -INFINITY) continue;
-                const float Mn = fmaxf(Mx, mv[q]);
-                const float fo = exp2f(Mx - Mn), fn = exp2f(mv[q] - Mn);
-                o = o * fo + ov[q] * fn;
-                l = l * fo + lv[q] * fn;
-                Mx = Mn;
-              }
-            }
-            stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
-          }
-        }
-      }
       __syncthreads();
     }
     i = inext;
   }
+  STEP_TRACE(p, 6);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -999,10 +1008,10 @@ __device__ __forceinline__ int phase_kind(const Args& a, int p, int* layer) {
   return P_QKV + (p - 1) % 5;
 }
 
-__device__ __forceinline__ bool phase_geo(const Args& a, int p, Geo* g) {
+__device__ __forceinline__ bool phase_geo(const Args& a, const Shared& sh, int p, Geo* g) {
   int layer;
   const int kind = phase_kind(a, p, &layer);
-  const int64_t* lp = layer >= 0 ? a.layers + (size_t)layer * NFIELD : nullptr;
+  const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
   switch (kind) {
     case P_QKV: *g = make_geo((const bf16*)lp[F_WQKV], (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV, true); return true;
     case P_O:   *g = make_geo((const bf16*)lp[F_WO], a.H, a.NH * HD, LNR_O, false); return true;
@@ -1013,9 +1022,146 @@ __device__ __forceinline__ bool phase_geo(const Args& a, int p, Geo* g) {
   }
 }
 
+// Staging of the O projection's input x = the attention output of `layer`. A (row, kv head)
+// split over attention workgroups is combined here from its (o, m, l) partials (log-sum-exp,
+// online in workgroup order) on the way into LDS, and also written to the attention slot.
+// The partials are write-once per layer (plain cached loads); every load of a thread's items
+// is issued before the first combine.
+constexpr int SA_IPT = 3;            // items per thread per batch
+
+__device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
+                                           int layer, int p) {
+  const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
+  const int K = NH * HD;
+  const int t = tid();
+  int ksf = 0, nw = 0;
+  if (g.s1 > g.s0) {
+    ksf = g.s0 % g.nk;
+    nw = min(g.s1 - g.s0, g.nk);
+  }
+  const int xrs = nw * 64 + 16;
+  const int items = M * nw * 4;
+  attn_partition(a, sh, false);
+  STEP_TRACE(p, 4);
+  const int T = sh.units[M];
+  const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * K * 2));
+  const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
+  if (t == 0) {
+    sh.xrs = xrs;
+    sh.xksf = ksf;
+    sh.xnw = nw;
+  }
+  // per (row, kv head): contributor range and the first SA_PQ contributors' record offsets
+  constexpr int SA_PQ = 3;
+  const int gsh = __builtin_ctz(G);
+  for (int pi = t; pi < M * NKV; pi += NTHR) {
+    const int m = pi / NKV, kvh = pi - m * NKV;
+    const int64_t pp = sh.posv[m];
+    const int Lb = (int)min<int64_t>(max<int64_t>(pp + 1, 0), (int64_t)a.cap);
+    const int nblk = (Lb + 31) >> 5;
+    int* pin = sh.pinfo[pi];
+    if (nblk == 0) {
+      pin[0] = 0;
+      pin[1] = -1;                                                  // no keys: zeros
+      for (int q = 0; q < SA_PQ; ++q) pin[2 + q] = -1;
+      continue;
+    }
+    const int S = sh.units[m] + kvh * (ATT_OVH + nblk);
+    const int fw = attn_owner(T, S + ATT_OVH), lw = attn_owner(T, S + ATT_OVH + nblk - 1);
+    pin[0] = fw;
+    pin[1] = lw;
+#pragma unroll
+    for (int q = 0; q < SA_PQ; ++q) {
+      const int c = fw + q;
+      const bool ok = lw > fw && c <= lw && sh.afirst[c + 1] > sh.afirst[c];
+      pin[2 + q] = ok ? (int)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G) * ATT_REC * 4) : -1;
+    }
+    pin[6] = S;
+  }
+  __syncthreads();
+  for (int base = 0; base < items; base += SA_IPT * NTHR) {
+    int lds[SA_IPT], m_[SA_IPT], pi_[SA_IPT], hh_[SA_IPT], d0_[SA_IPT];
+    unsigned eo_[SA_IPT];
+    u32x4 xd[SA_IPT];
+    float mv[SA_IPT][SA_PQ], lv[SA_IPT][SA_PQ];
+    u32x4 oa[SA_IPT][SA_PQ], ob[SA_IPT][SA_PQ];
+    // pass 1: every load
+#pragma unroll
+    for (int b = 0; b < SA_IPT; ++b) {
+      const int it = base + t + b * NTHR;
+      const bool valid = it < items;
+      const unsigned eo = stage_off(valid ? it : 0, nw > 0 ? nw : 1, ksf, g.nk > 0 ? g.nk : 1, K, &lds[b]);
+      const int m = valid ? it / (nw * 4) : 0;
+      const int col = (int)(eo - (unsigned)m * K);
+      const int h = col >> 7, kvh = h >> gsh;
+      hh_[b] = h & (G - 1);
+      d0_[b] = col & (HD - 1);
+      m_[b] = valid ? m : -1;
+      eo_[b] = eo;
+      const int pi = m * NKV + kvh;
+      pi_[b] = pi;
+      const int fw = sh.pinfo[pi][0], lw = sh.pinfo[pi][1];
+      xd[b] = ldb128(orr, valid && fw == lw ? eo * 2 : 0xfffffff0u);
+      const unsigned hoff = (unsigned)(hh_[b] * ATT_REC * 4);
+#pragma unroll
+      for (int q = 0; q < SA_PQ; ++q) {
+        const int r = sh.pinfo[pi][2 + q];
+        const bool ok = valid && r >= 0;
+        const unsigned ro = (unsigned)r + hoff;
+        mv[b][q] = ok ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + HD * 4, 0, 0)) : -INFINITY;
+        lv[b][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ok ? ro + (HD + 1) * 4 : 0xfffffff0u, 0, 0));
+        oa[b][q] = ldb128(pr, ok ? ro + d0_[b] * 4 : 0xfffffff0u);
+        ob[b][q] = ldb128(pr, ok ? ro + (d0_[b] + 4) * 4 : 0xfffffff0u);
+      }
+    }
+    // pass 2: combine (contributors beyond the first SA_PQ are loaded here, rarely)
+#pragma unroll
+    for (int b = 0; b < SA_IPT; ++b) {
+      if (m_[b] < 0) continue;
+      const int pi = pi_[b];
+      const int fw = sh.pinfo[pi][0], lw = sh.pinfo[pi][1];
+      u32x4 x = xd[b];
+      if (lw > fw) {
+        float Mx = -INFINITY, l = 0.f, o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = 0.f;
+        auto add = [&](float mq, float lq, u32x4 qa, u32x4 qb) {
+          if (mq == -INFINITY) return;
+          const float Mn = fmaxf(Mx, mq);
+          const float fo = exp2f(Mx - Mn), fn = exp2f(mq - Mn);
+          const float ov[8] = {__uint_as_float(qa.x), __uint_as_float(qa.y), __uint_as_float(qa.z),
+                               __uint_as_float(qa.w), __uint_as_float(qb.x), __uint_as_float(qb.y),
+                               __uint_as_float(qb.z), __uint_as_float(qb.w)};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[j] = o[j] * fo + ov[j] * fn;
+          l = l * fo + lq * fn;
+          Mx = Mn;
+        };
+#pragma unroll
+        for (int q = 0; q < SA_PQ; ++q) add(mv[b][q], lv[b][q], oa[b][q], ob[b][q]);
+        const int S = sh.pinfo[pi][6];
+        for (int c = fw + SA_PQ; c <= lw; ++c) {
+          if (sh.afirst[c + 1] <= sh.afirst[c]) continue;
+          const unsigned ro = (unsigned)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G + hh_[b]) * ATT_REC) * 4;
+          add(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + HD * 4, 0, 0)),
+              __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + (HD + 1) * 4, 0, 0)),
+              ldb128(pr, ro + d0_[b] * 4), ldb128(pr, ro + (d0_[b] + 4) * 4));
+        }
+        x = u32x4{pk_bf16(o[0] / l, o[1] / l), pk_bf16(o[2] / l, o[3] / l),
+                  pk_bf16(o[4] / l, o[5] / l), pk_bf16(o[6] / l, o[7] / l)};
+        stc_b128(orr, eo_[b] * 2, x);
+      }
+      *(u32x4*)(xb + m_[b] * xrs + lds[b]) = x;
+    }
+  }
+  STEP_TRACE(p, 5);
+  STEP_TRACE(p, 6);
+  __syncthreads();
+}
+
 // One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, stage
 // the activation window, consume. The prefetch registers live only inside this call.
-template <int LNR, int EPI>
+template <int LNR, int EPI, bool ATTN_X = false>
 __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g, int p, int layer,
                                          bool sync, unsigned epoch, int K, const bf16* src,
                                          const bf16* lnw, const float* ss) {
@@ -1027,7 +1173,8 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g
   issue_batch<NR>(g, BATCH / NR, B);
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
-  stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss, p);
+  if (ATTN_X) stage_attn(a, sh, GemvLds<NR>(sh).x, g, layer >> 1, p);   // layer: output h slot 2l+1
+  else stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss, p);
   STEP_TRACE(p, 2);
   gemv_phase<NR, EPI>(a, sh, g, layer, A, B);
   STEP_TRACE(p, 3);
@@ -1042,22 +1189,25 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
     sh.besti[tid()] = 0x7fffffff;
   }
   if (tid() == 0) sh.bail = 0;
+  if (tid() < a.M) sh.posv[tid()] = a.pos[tid()];
+  for (int e = tid(); e < a.L * LFIELDS; e += NTHR)
+    sh.ltab[e / LFIELDS][e % LFIELDS] = a.layers[(size_t)(e / LFIELDS) * NFIELD + e % LFIELDS];
   __syncthreads();
   for (int p = a.phase_begin; p < a.phase_end; ++p) {
     int layer;
     const int kind = phase_kind(a, p, &layer);
-    const int64_t* lp = layer >= 0 ? a.layers + (size_t)layer * NFIELD : nullptr;
+    const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
     const bool sync = p > a.phase_begin;
     if (sync) ++epoch;
     Geo g;
-    phase_geo(a, p, &g);
+    phase_geo(a, sh, p, &g);
     switch (kind) {
       case P_QKV:
         run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer),
                                    (const bf16*)lp[F_LN1], ss_slot(a, 2 * layer));
         break;
       case P_O:
-        run_gemv<LNR_O, EPI_RES>(a, sh, g, p, 2 * layer + 1, sync, epoch, a.NH * HD,
+        run_gemv<LNR_O, EPI_RES, true>(a, sh, g, p, 2 * layer + 1, sync, epoch, a.NH * HD,
                                  attn_slot(a, layer), nullptr, nullptr);
         break;
       case P_GU:
@@ -1080,7 +1230,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
         }
         STEP_TRACE(p, 1);
         if (kind == P_EMB) embed_phase(a, sh);
-        else attention_phase(a, sh, layer);
+        else attention_phase(a, sh, layer, p);
         STEP_TRACE(p, 3);
         break;
     }
@@ -1092,25 +1242,25 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
         stc_u32(cr, (unsigned)((blockIdx.x * MAXM + tid()) * 2 + 1) * 4, (unsigned)sh.besti[tid()]);
       }
       if (arrive_last(a.ctr + C_AM, gridDim.x, &sh.flag)) {
-        if (tid() < 64) {
-          for (int m = 0; m < a.M; ++m) {
-            float bv = -INFINITY;
-            int bi = 0x7fffffff;
-            for (int w = tid(); w < (int)gridDim.x; w += 64) {
-              const float v = ldc_f32(cr, (unsigned)((w * MAXM + m) * 2) * 4);
-              const int i = (int)ldc_u32(cr, (unsigned)((w * MAXM + m) * 2 + 1) * 4);
-              if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
-            }
+        // one wave per row: lanes scan the workgroups' candidates, then a wave reduction
+        const int lane = tid() & 63;
+        for (int m = wave_id(); m < a.M; m += NWAVE) {
+          float bv = -INFINITY;
+          int bi = 0x7fffffff;
+          for (int w = lane; w < (int)gridDim.x; w += 64) {
+            const float v = ldc_f32(cr, (unsigned)((w * MAXM + m) * 2) * 4);
+            const int i = (int)ldc_u32(cr, (unsigned)((w * MAXM + m) * 2 + 1) * 4);
+            if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+          }
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-              const float ov = __shfl_xor(bv, o, 64);
-              const int oi = __shfl_xor(bi, o, 64);
-              if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
-            if (tid() == 0) {
-              a.tok[m] = bi;
-              a.pos[m] += 1;
-            }
+          for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+          }
+          if (lane == 0) {
+            a.tok[m] = bi;
+            a.pos[m] = sh.posv[m] + 1;
           }
         }
       }
@@ -1182,6 +1332,7 @@ static int step_grid(int* G_out) {
       hipSuccess || occ < 1)
     return (int)hipErrorInvalidConfiguration;
   *G_out = cus & ~7;   // barrier groups workgroups by XCD (8 per device)
+  if (*G_out < 8 || *G_out > MAXG) return (int)hipErrorInvalidConfiguration;
   return 0;
 }
 
@@ -1192,7 +1343,7 @@ static WsLayout ws_layout(int L, int G, int G_heads) {
   w.ss = 0;
   w.part = (size_t)(2 * L + 1) * SS_SLOT;                   // ss: [2L+1][H/64 <= 64][16]
   w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // GEMV: 2 slots of <= 128 rows x 16
-  w.am = w.att + (size_t)G * 2 * G_heads * (HD + 2);        // attention: 2 slots of G heads
+  w.am = w.att + (size_t)L * G * 2 * G_heads * ATT_REC;    // attention: per layer, 2 slots
   w.total = w.am + (size_t)G * MAXM * 2;
   return w;
 }
@@ -1234,7 +1385,7 @@ DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int 
 // GEMV phase's staged activation window fits the LDS x buffer with that many workgroups.
 static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int G) {
   if (!(M >= 1 && M <= MAXM && L >= 1 && NKV >= 1 && NH >= NKV && NH % NKV == 0 &&
-        NH / NKV <= 16))
+        NH / NKV <= MAXG_HEADS && ((NH / NKV) & (NH / NKV - 1)) == 0 && L <= MAXL))
     return false;
   if (MAXM * NKV > C_AM - C_ATT) return false;            // one combine counter per (row, kv head)
   if (!(H % SSG == 0 && H / SSG <= 64 && I % 16 == 0 && V % 32 == 0)) return false;
@@ -1253,6 +1404,7 @@ static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int 
       const long long per = (S + G - 1) / G;
       const long long nw = whole_of[q] || per > nk ? nk : per;
       if ((nw * 64 + 16) * M > (long long)x_capacity(1 << lnr)) return false;
+      if (S * (G + 1) >= (1ll << 31)) return false;           // 32-bit partition arithmetic
     }
   }
   return true;
@@ -1279,6 +1431,8 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   const int e = step_grid(&G);
   if (e != 0) return e;
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, G));
+  // attention partition units (32-bit arithmetic in the kernel)
+  DD_REQUIRE((long long)MAXM * NKV * (ATT_OVH + cap / 32 + 1) * (G + 1) < (1ll << 31));
   const WsLayout w = ws_layout(L, G, NH / NKV);
   Args a;
   a.layers = layer_table;

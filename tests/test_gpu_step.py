@@ -221,10 +221,12 @@ def test_fused_phases_per_kernel(cuda, shape):
         idx = pos.view(B, 1, 1, 1).expand(B, eng.nkv, 1, 128)
         _close(c.gather(2, idx), rc.gather(2, idx), f"{name} write (norm + rope)")
     o = ops.attn_decode_rows(q, st.kc[0].cpu(), st.vc[0].cpu(), pos)
-    _close(cpu(f.attn[0]), o, "attention")
 
+    # O + residual; a (row, kv head) split over attention workgroups is combined from its
+    # partials while O stages its input (and written to the attention slot there)
+    eng.step.run(st, 3, 4)
     attn = cpu(f.attn[0])
-    eng.step.run(st, 3, 4)                                   # O + residual
+    _close(attn, o, "attention")
     h1 = cpu(f.h[1])
     want_h1, _ = ops.linear_add_norm(attn, rl.wo, h, rl.ln2)
     _close(h1, want_h1, "O + residual")
