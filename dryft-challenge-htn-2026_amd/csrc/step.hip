@@ -227,6 +227,7 @@ struct Shared {
   int nseg, segnext;
   long long posv[MAXM];                       // this step's positions (read once at launch)
   int afirst[MAXG + 1];                       // attention: first unit of each workgroup
+  int aG;                                     // attention: workgroups holding units
   long long ltab[MAXL][LFIELDS];              // the layer table, copied once per launch
   int pinfo[MAXM * 32][8];                    // O staging: per (row, kv head) fw, lw, record
                                               // offsets of its first 3 contributors (-1: none), S
@@ -497,7 +498,7 @@ __device__ __forceinline__ void run_epilogue(const Args& a, Shared& sh, float (*
 // adds +0).
 template <int NR, int EPI>
 __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
-                            f32x4 (&acc)[NR]) {
+                            f32x4 (&acc)[NR], int p = -1) {
   const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
   GemvLds<NR> L(sh);
@@ -536,10 +537,12 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
     // contributors: the workgroups first..last whose step range is not empty
     int ncontrib = 0;
     for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
+    STEP_TRACE(p, 4);
     finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
+    STEP_TRACE(p, 5);
     if (finish) {
       constexpr int EPT = (NR * 16 * MAXM + NTHR - 1) / NTHR;
-      constexpr int CB = 4;
+      constexpr int CB = 8;
       float acc[EPT];
 #pragma unroll
       for (int i = 0; i < EPT; ++i) acc[i] = 0.f;
@@ -571,9 +574,11 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
         if (e < rows * M) L.res[e / M][e % M] = acc[i];
       }
       __syncthreads();
+      STEP_TRACE(p, 6);
     }
   }
   if (finish) run_epilogue<EPI>(a, sh, L.res, grp, layer);
+  if (finish && first != last) STEP_TRACE(p, 7);
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
 }
@@ -613,9 +618,9 @@ __device__ __forceinline__ void gemv_consume(const Geo& g, const u32x4 (&buf)[BA
 template <int NR, int EPI>
 __device__ __forceinline__ void gemv_flush_to(const Args& a, Shared& sh, const Geo& g, int layer,
                                               int target, int seg0, int& flushed,
-                                              f32x4 (&cur)[NR], f32x4 (&nxt)[NR]) {
+                                              f32x4 (&cur)[NR], f32x4 (&nxt)[NR], int p) {
   while (flushed < target) {
-    flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, cur);   // leaves cur zeroed
+    flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, cur, p);   // leaves cur zeroed
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
       cur[t] = nxt[t];
@@ -629,7 +634,7 @@ __device__ __forceinline__ void gemv_flush_to(const Args& a, Shared& sh, const G
 // batches 0 and 1; batches alternate between them. Returns with nothing in flight.
 template <int NR, int EPI>
 __device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo& g, int layer,
-                                           u32x4 (&A)[BATCH], u32x4 (&B)[BATCH]) {
+                                           u32x4 (&A)[BATCH], u32x4 (&B)[BATCH], int p) {
   constexpr int U = BATCH / NR;   // steps per batch
   const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
@@ -654,7 +659,7 @@ __device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo&
       issue_batch<NR>(g, j0 + 2 * U, A);
       __builtin_amdgcn_sched_barrier(0);    // keep the refill ahead of the next batch's MFMAs
       gemv_flush_to<NR, EPI>(a, sh, g, layer, grp_of(min(j0 + U, nmine) - 1), seg0, flushed,
-                             cur, nxt);
+                             cur, nxt, p);
     }
     if (j0 + U < nmine) {
       gemv_consume<NR>(g, B, j0 + U, nmine, seg0 + flushed, xrow_p, ksf, cur, nxt);
@@ -664,7 +669,7 @@ __device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo&
     const bool done = j0 + 2 * U >= nmine;
     gemv_flush_to<NR, EPI>(a, sh, g, layer,
                            done ? nseg : grp_of(min(j0 + 2 * U, nmine) - 1), seg0, flushed,
-                           cur, nxt);
+                           cur, nxt, p);
     if (done) break;
   }
 }
@@ -700,12 +705,16 @@ __device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& 
   }
 }
 
-// Partition arithmetic stays in 32 bits (units x workgroups < 2^31, checked on the host).
-__device__ __forceinline__ int attn_owner(int T, int i) {          // workgroup of global unit i
-  return (int)(((unsigned)(i + 1) * gridDim.x - 1) / (unsigned)T);
+// The units are split over the first Ga workgroups, Ga = min(grid, T / ATT_MINU): a small
+// workload (short contexts, B = 1) stays on fewer workgroups, so a (row, kv head) is split over
+// few contributors. Partition arithmetic stays in 32 bits (units x workgroups < 2^31, checked
+// on the host).
+constexpr int ATT_MINU = 16;
+__device__ __forceinline__ int attn_owner(int T, int Ga, int i) {  // workgroup of global unit i
+  return (int)(((unsigned)(i + 1) * Ga - 1) / (unsigned)T);
 }
-__device__ __forceinline__ int attn_first(int T, int c) {          // first unit of workgroup c
-  return (int)((unsigned)T * c / gridDim.x);
+__device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit of workgroup c
+  return c >= Ga ? T : (int)((unsigned)T * c / Ga);
 }
 
 // Partition units of one (row, kv head): ATT_OVH units for its fixed per-segment latency
@@ -738,7 +747,9 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
   }
   __syncthreads();
   const int T = sh.units[a.M];
-  for (int c = tid(); c <= (int)gridDim.x; c += NTHR) sh.afirst[c] = attn_first(T, c);
+  const int Ga = max(1, min((int)gridDim.x, T / ATT_MINU));
+  for (int c = tid(); c <= (int)gridDim.x; c += NTHR) sh.afirst[c] = attn_first(T, Ga, c);
+  if (tid() == 0) sh.aG = Ga;
   __syncthreads();
 }
 
@@ -756,7 +767,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   attn_partition(a, sh, true);
   STEP_TRACE(p, 4);
   const int T = sh.units[M];
-  const int i0 = attn_first(T, blockIdx.x), i1 = attn_first(T, blockIdx.x + 1);
+  const int i0 = sh.afirst[blockIdx.x], i1 = sh.afirst[blockIdx.x + 1];
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
   const rsrc_t rawr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
@@ -1067,7 +1078,7 @@ __device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned c
       continue;
     }
     const int S = sh.units[m] + kvh * (ATT_OVH + nblk);
-    const int fw = attn_owner(T, S + ATT_OVH), lw = attn_owner(T, S + ATT_OVH + nblk - 1);
+    const int fw = attn_owner(T, sh.aG, S + ATT_OVH), lw = attn_owner(T, sh.aG, S + ATT_OVH + nblk - 1);
     pin[0] = fw;
     pin[1] = lw;
 #pragma unroll
@@ -1176,7 +1187,7 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g
   if (ATTN_X) stage_attn(a, sh, GemvLds<NR>(sh).x, g, layer >> 1, p);   // layer: output h slot 2l+1
   else stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss, p);
   STEP_TRACE(p, 2);
-  gemv_phase<NR, EPI>(a, sh, g, layer, A, B);
+  gemv_phase<NR, EPI>(a, sh, g, layer, A, B, p);
   STEP_TRACE(p, 3);
 }
 
