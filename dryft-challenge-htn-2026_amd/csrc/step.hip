@@ -68,7 +68,7 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 
 // Optional timing trace (compiled in only with -DDD_STEP_TRACE, for profiling builds): wall
 // clock (100 MHz) per workgroup at phase milestones, read back with dd_step_trace.
-constexpr int TR_PHASES = 192, TR_EVENTS = 8;
+constexpr int TR_PHASES = 192, TR_EVENTS = 12;
 #ifdef DD_STEP_TRACE
 __device__ unsigned long long g_trace[1024 * TR_PHASES * TR_EVENTS];
 #define STEP_TRACE(p, ev)                                                                    \
@@ -359,7 +359,7 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
       sh.rs[t] = rsqrt_ieee(r / (float)a.H + a.eps);
     }
   }
-  STEP_TRACE(p, 5);
+  STEP_TRACE(p, 8);
   if (t == 0) {
     sh.xrs = xrs;
     sh.xksf = ksf;
@@ -390,7 +390,7 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
       *(u32x4*)(xb + m * xrs + lo_[b]) = x;
     }
   }
-  STEP_TRACE(p, 6);
+  STEP_TRACE(p, 9);
   __syncthreads();
 }
 
@@ -529,11 +529,10 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
     const unsigned slot_floats = (unsigned)(rows * MAXM);
     const rsrc_t pr = make_rsrc(a.ws + a.off_part, (unsigned)(gridDim.x * 2 * slot_floats * 4));
     const int myslot = (grp == g.s0 / g.nk) ? 0 : 1;
-    for (int e = tid(); e < rows * M; e += NTHR) {
-      const int row = e / M, m = e - (e / M) * M;
-      stc_f32(pr, ((blockIdx.x * 2 + myslot) * slot_floats + row * MAXM + m) * 4,
-              L.res[row][m]);
-    }
+    // whole [rows][MAXM] tiles (columns >= M carry finite values nobody reads): no division
+    constexpr int PE = NR * 16 * MAXM;       // floats per partial
+    const unsigned mybase = (blockIdx.x * 2 + myslot) * slot_floats * 4;
+    for (int e = tid(); e < PE; e += NTHR) stc_f32(pr, mybase + e * 4, L.res[e >> 4][e & 15]);
     // contributors: the workgroups first..last whose step range is not empty
     int ncontrib = 0;
     for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
@@ -541,27 +540,30 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
     finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
     STEP_TRACE(p, 5);
     if (finish) {
-      constexpr int EPT = (NR * 16 * MAXM + NTHR - 1) / NTHR;
+      constexpr int EPT = (PE + NTHR - 1) / NTHR;
       constexpr int CB = 8;
+      constexpr unsigned NONE = 0x80000000u;  // past the descriptor's range: reads 0
       float acc[EPT];
 #pragma unroll
       for (int i = 0; i < EPT; ++i) acc[i] = 0.f;
       for (int c0 = first; c0 <= last; c0 += CB) {
-        float pv[EPT][CB];
+        // contributor record bases (workgroup-uniform), then every load unconditional
+        unsigned cb[CB];
+        int cs = step0_of(g, c0);
 #pragma unroll
         for (int j = 0; j < CB; ++j) {
           const int c = c0 + j;
-          const int cs0 = step0_of(g, c);
-          const bool ok = c <= last && step0_of(g, c + 1) > cs0;
-          const int slot = (grp == cs0 / g.nk) ? 0 : 1;
+          const int cn = step0_of(g, c + 1);
+          const bool ok = c <= last && cn > cs;
+          cb[j] = ok ? (unsigned)((c * 2 + (cs >= grp * g.nk ? 0 : 1)) * slot_floats * 4) : NONE;
+          cs = cn;
+        }
+        float pv[EPT][CB];
 #pragma unroll
-          for (int i = 0; i < EPT; ++i) {
-            const int e = tid() + i * NTHR;
-            const int row = e / M, m = e - row * M;
-            pv[i][j] = ok && e < rows * M
-                           ? ldc_f32(pr, ((c * 2 + slot) * slot_floats + row * MAXM + m) * 4)
-                           : 0.f;
-          }
+        for (int i = 0; i < EPT; ++i) {
+          const int e = tid() + i * NTHR;
+#pragma unroll
+          for (int j = 0; j < CB; ++j) pv[i][j] = ldc_f32(pr, (e < PE ? cb[j] : NONE) + e * 4);
         }
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
@@ -571,7 +573,7 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
 #pragma unroll
       for (int i = 0; i < EPT; ++i) {
         const int e = tid() + i * NTHR;
-        if (e < rows * M) L.res[e / M][e % M] = acc[i];
+        if (e < PE) L.res[e >> 4][e & 15] = acc[i];
       }
       __syncthreads();
       STEP_TRACE(p, 6);
@@ -1053,7 +1055,7 @@ __device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned c
   const int xrs = nw * 64 + 16;
   const int items = M * nw * 4;
   attn_partition(a, sh, false);
-  STEP_TRACE(p, 4);
+  STEP_TRACE(p, 8);
   const int T = sh.units[M];
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * K * 2));
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
@@ -1158,15 +1160,17 @@ __device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned c
               __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + (HD + 1) * 4, 0, 0)),
               ldb128(pr, ro + d0_[b] * 4), ldb128(pr, ro + (d0_[b] + 4) * 4));
         }
-        x = u32x4{pk_bf16(o[0] / l, o[1] / l), pk_bf16(o[2] / l, o[3] / l),
-                  pk_bf16(o[4] / l, o[5] / l), pk_bf16(o[6] / l, o[7] / l)};
-        stc_b128(orr, eo_[b] * 2, x);
+        const float il = 1.0f / l;
+        x = u32x4{pk_bf16(o[0] * il, o[1] * il), pk_bf16(o[2] * il, o[3] * il),
+                  pk_bf16(o[4] * il, o[5] * il), pk_bf16(o[6] * il, o[7] * il)};
+        // the attention slot copy is written by one workgroup only: the one whose range holds
+        // this k-step of row group 0
+        if (g.s0 + (lds[b] >> 6) < g.nk) stc_b128(orr, eo_[b] * 2, x);
       }
       *(u32x4*)(xb + m_[b] * xrs + lds[b]) = x;
     }
   }
-  STEP_TRACE(p, 5);
-  STEP_TRACE(p, 6);
+  STEP_TRACE(p, 9);
   __syncthreads();
 }
 
@@ -1476,7 +1480,7 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
 }
 
 #ifdef DD_STEP_TRACE
-// Profiling builds only: copy the timing trace ([1024][192][4] u64) to host memory.
+// Profiling builds only: copy the timing trace ([1024][192][12] u64) to host memory.
 DD_API int dd_step_trace(void* host, size_t bytes) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes, 0, hipMemcpyDeviceToHost);
 }
