@@ -296,9 +296,21 @@ __device__ __forceinline__ unsigned stage_off(int it, int nw, int ksf, int nk, i
   return (unsigned)((size_t)m * K + ks * 32 + e * 8);
 }
 
+// The norm weight of the window does not depend on the previous phase: its load is issued before
+// the barrier wait (thread t < 4 * window holds 16 bytes of k-step t / 4).
+__device__ __forceinline__ u32x4 lnw_prefetch(const Geo& g, const bf16* lnw, int K) {
+  const int t = tid();
+  const int ksf = g.s1 > g.s0 ? g.s0 % g.nk : 0;
+  const int nw = g.s1 > g.s0 ? min(g.s1 - g.s0, g.nk) : 0;
+  int ks = ksf + (t >> 2);
+  if (ks >= g.nk) ks -= g.nk;
+  const rsrc_t r = make_rsrc(lnw, (unsigned)(K * 2));
+  return ldb128(r, t < nw * 4 ? (unsigned)((ks * 32 + (t & 3) * 8) * 2) : 0xfffffff0u);
+}
+
 __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
-                                        int K, const bf16* src, const bf16* lnw, const float* ss,
-                                        int p) {
+                                        int K, const bf16* src, const bf16* lnw, u32x4 lwv,
+                                        const float* ss, int p) {
   const int M = a.M;
   const int t = tid();
   int ksf = 0, nw = 0;
@@ -335,15 +347,9 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
     }
   };
   issue();
-  // a norm window beyond the LDS copy (only with fewer workgroups than the window needs) is
-  // read from global memory per item instead
-  const bool lnw_lds = lnw != nullptr && nw <= LNW_KS;
+  // norm phases have K = H <= 64 * SSG (checked on the host): the window fits LNW_KS k-steps
   if (lnw != nullptr) {
-    if (lnw_lds && t < nw * 4) {
-      int ks = ksf + (t >> 2);
-      if (ks >= g.nk) ks -= g.nk;
-      *(u32x4*)&sh.lnw[t * 8] = ld16(lnw + ks * 32 + (t & 3) * 8);
-    }
+    if (t < nw * 4) *(u32x4*)&sh.lnw[t * 8] = lwv;
     // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): thread (p, m) sums groups p, p + 32, ...; then
     // row m adds the 32 partials in order
     const int m = t & (MAXM - 1), p = t / MAXM;
@@ -375,11 +381,7 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
       u32x4 x = v[b];
       if (lnw != nullptr) {
         const float r = sh.rs[m];
-        const int w = lo_[b] >> 6, e = (lo_[b] >> 4) & 3;
-        int ks = ksf + w;
-        if (ks >= g.nk) ks -= g.nk;
-        const u32x4 wv = lnw_lds ? *(const u32x4*)&sh.lnw[(lo_[b] >> 4) * 8]
-                                 : ld16(lnw + ks * 32 + e * 8);
+        const u32x4 wv = *(const u32x4*)&sh.lnw[(lo_[b] >> 4) * 8];
         const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
         unsigned o[4];
 #pragma unroll
@@ -725,6 +727,8 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 constexpr int ATT_OVH = 12;
 constexpr int ATT_REC = HD + 4;      // split partial record: o[128], m, l, 2 pad (16-byte rows)
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
+constexpr int SA_PQ = 3;             // contributors per (row, kv head) whose records the O
+                                     // staging loads in its first pass
 
 // units[b]: first partition unit of row b (rows with no keys have none); units[M] = total
 __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool flag_errors) {
@@ -755,6 +759,40 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
   __syncthreads();
 }
 
+// The attention partition depends only on this step's positions: computed once per launch,
+// with the O staging's per-(row, kv head) contributor table (fw, lw, record offsets of the
+// first contributors, S).
+__device__ __forceinline__ void attn_setup(const Args& a, Shared& sh, bool flag_errors) {
+  const int M = a.M, NKV = a.NKV, G = a.NH / a.NKV;
+  attn_partition(a, sh, flag_errors);
+  const int T = sh.units[M];
+  for (int pi = tid(); pi < M * NKV; pi += NTHR) {
+    const int m = pi / NKV, kvh = pi - m * NKV;
+    const int64_t pp = sh.posv[m];
+    const int Lb = (int)min<int64_t>(max<int64_t>(pp + 1, 0), (int64_t)a.cap);
+    const int nblk = (Lb + 31) >> 5;
+    int* pin = sh.pinfo[pi];
+    if (nblk == 0) {
+      pin[0] = 0;
+      pin[1] = -1;                                                  // no keys: zeros
+      for (int q = 0; q < SA_PQ; ++q) pin[2 + q] = -1;
+      continue;
+    }
+    const int S = sh.units[m] + kvh * (ATT_OVH + nblk);
+    const int fw = attn_owner(T, sh.aG, S + ATT_OVH), lw = attn_owner(T, sh.aG, S + ATT_OVH + nblk - 1);
+    pin[0] = fw;
+    pin[1] = lw;
+#pragma unroll
+    for (int q = 0; q < SA_PQ; ++q) {
+      const int c = fw + q;
+      const bool ok = lw > fw && c <= lw && sh.afirst[c + 1] > sh.afirst[c];
+      pin[2 + q] = ok ? (int)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G) * ATT_REC * 4) : -1;
+    }
+    pin[6] = S;
+  }
+  __syncthreads();
+}
+
 __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer, int p) {
   const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
   const int lane = tid() & 63, wave = wave_id();
@@ -766,9 +804,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const bf16* knw = (const bf16*)lp[F_KN];
   const int nqkv = (NH + 2 * NKV) * HD;
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
-  attn_partition(a, sh, true);
   STEP_TRACE(p, 4);
-  const int T = sh.units[M];
   const int i0 = sh.afirst[blockIdx.x], i1 = sh.afirst[blockIdx.x + 1];
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
@@ -1054,9 +1090,7 @@ __device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned c
   }
   const int xrs = nw * 64 + 16;
   const int items = M * nw * 4;
-  attn_partition(a, sh, false);
   STEP_TRACE(p, 8);
-  const int T = sh.units[M];
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * K * 2));
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
   if (t == 0) {
@@ -1064,34 +1098,7 @@ __device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned c
     sh.xksf = ksf;
     sh.xnw = nw;
   }
-  // per (row, kv head): contributor range and the first SA_PQ contributors' record offsets
-  constexpr int SA_PQ = 3;
   const int gsh = __builtin_ctz(G);
-  for (int pi = t; pi < M * NKV; pi += NTHR) {
-    const int m = pi / NKV, kvh = pi - m * NKV;
-    const int64_t pp = sh.posv[m];
-    const int Lb = (int)min<int64_t>(max<int64_t>(pp + 1, 0), (int64_t)a.cap);
-    const int nblk = (Lb + 31) >> 5;
-    int* pin = sh.pinfo[pi];
-    if (nblk == 0) {
-      pin[0] = 0;
-      pin[1] = -1;                                                  // no keys: zeros
-      for (int q = 0; q < SA_PQ; ++q) pin[2 + q] = -1;
-      continue;
-    }
-    const int S = sh.units[m] + kvh * (ATT_OVH + nblk);
-    const int fw = attn_owner(T, sh.aG, S + ATT_OVH), lw = attn_owner(T, sh.aG, S + ATT_OVH + nblk - 1);
-    pin[0] = fw;
-    pin[1] = lw;
-#pragma unroll
-    for (int q = 0; q < SA_PQ; ++q) {
-      const int c = fw + q;
-      const bool ok = lw > fw && c <= lw && sh.afirst[c + 1] > sh.afirst[c];
-      pin[2 + q] = ok ? (int)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G) * ATT_REC * 4) : -1;
-    }
-    pin[6] = S;
-  }
-  __syncthreads();
   for (int base = 0; base < items; base += SA_IPT * NTHR) {
     int lds[SA_IPT], m_[SA_IPT], pi_[SA_IPT], hh_[SA_IPT], d0_[SA_IPT];
     unsigned eo_[SA_IPT];
@@ -1186,10 +1193,11 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g
   if (sync) bar_arrive(a, epoch);
   issue_batch<NR>(g, 0, A);
   issue_batch<NR>(g, BATCH / NR, B);
+  const u32x4 lwv = (!ATTN_X && lnw != nullptr) ? lnw_prefetch(g, lnw, K) : u32x4{0u, 0u, 0u, 0u};
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
   if (ATTN_X) stage_attn(a, sh, GemvLds<NR>(sh).x, g, layer >> 1, p);   // layer: output h slot 2l+1
-  else stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, ss, p);
+  else stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, lwv, ss, p);
   STEP_TRACE(p, 2);
   gemv_phase<NR, EPI>(a, sh, g, layer, A, B, p);
   STEP_TRACE(p, 3);
@@ -1208,6 +1216,11 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
   for (int e = tid(); e < a.L * LFIELDS; e += NTHR)
     sh.ltab[e / LFIELDS][e % LFIELDS] = a.layers[(size_t)(e / LFIELDS) * NFIELD + e % LFIELDS];
   __syncthreads();
+  {
+    // attention phases are p = 2 + 5l: position errors are flagged when one of them runs
+    const int l0 = a.phase_begin <= 2 ? 0 : (a.phase_begin - 2 + 4) / 5;
+    attn_setup(a, sh, l0 < a.L && 2 + 5 * l0 < a.phase_end);
+  }
   for (int p = a.phase_begin; p < a.phase_end; ++p) {
     int layer;
     const int kind = phase_kind(a, p, &layer);
