@@ -66,6 +66,16 @@ __device__ __forceinline__ int tid() {
 // Wave index within the workgroup, as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid() >> 6); }
 
+// A pointer read from LDS (the layer table) lands in vector registers; buffer descriptors built
+// from it would then be looped over per distinct value. It is the same in every lane: move it
+// to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(long long v) {
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)v >> 32));
+  return (T*)(((unsigned long long)hi << 32) | lo);
+}
+
 // Optional timing trace (compiled in only with -DDD_STEP_TRACE, for profiling builds): wall
 // clock (100 MHz) per workgroup at phase milestones, read back with dd_step_trace.
 constexpr int TR_PHASES = 192, TR_EVENTS = 12;
@@ -689,18 +699,16 @@ __device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo&
 // LDS, and a (row, kv head) split over workgroups is combined (log-sum-exp, in workgroup order)
 // by the last contributor to arrive.
 
-// q/k head RMSNorm (weight w) and RoPE at position p for one head held by a wave: lane l holds
-// dims l and l + 64. v (norm == false) passes through.
-__device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& x1, const bf16* w,
-                                               int64_t p, bool rope, int lane) {
+// q/k head RMSNorm and RoPE for one head held by a wave: lane l holds dims l and l + 64, with
+// the norm weight (w0, w1) and the position's cos/sin values (c0, c1, s0, s1) of those dims.
+__device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& x1, float w0,
+                                               float w1, float c0, float c1, float s0, float s1,
+                                               bool rope) {
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float r = rsqrt_ieee(ss / (float)HD + a.eps);
-  const float n0 = rbf(rbf(x0 * r) * bf2f(w[lane]));
-  const float n1 = rbf(rbf(x1 * r) * bf2f(w[lane + 64]));
+  const float n0 = rbf(rbf(x0 * r) * w0);
+  const float n1 = rbf(rbf(x1 * r) * w1);
   if (rope) {
-    const size_t cb = (size_t)p * HD;
-    const float c0 = bf2f(a.cos_t[cb + lane]), c1 = bf2f(a.cos_t[cb + lane + 64]);
-    const float s0 = bf2f(a.sin_t[cb + lane]), s1 = bf2f(a.sin_t[cb + lane + 64]);
     x0 = rbf(rbf(n0 * c0) + rbf(-n1 * s0));
     x1 = rbf(rbf(n1 * c1) + rbf(n0 * s1));
   } else {
@@ -798,10 +806,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const int lane = tid() & 63, wave = wave_id();
   const int l16 = lane & 15, g4 = lane >> 4;
   const long long* lp = sh.ltab[layer];
-  bf16* kc = (bf16*)lp[F_KC];
-  bf16* vc = (bf16*)lp[F_VC];
-  const bf16* qnw = (const bf16*)lp[F_QN];
-  const bf16* knw = (const bf16*)lp[F_KN];
+  bf16* kc = uniform_ptr<bf16>(lp[F_KC]);
+  bf16* vc = uniform_ptr<bf16>(lp[F_VC]);
+  const bf16* qnw = uniform_ptr<const bf16>(lp[F_QN]);
+  const bf16* knw = uniform_ptr<const bf16>(lp[F_KN]);
   const int nqkv = (NH + 2 * NKV) * HD;
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
   STEP_TRACE(p, 4);
@@ -809,6 +817,9 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
   const rsrc_t rawr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
+  const rsrc_t qwr = make_rsrc(qnw, HD * 2), kwr_n = make_rsrc(knw, HD * 2);
+  const rsrc_t cosr = make_rsrc(a.cos_t, (unsigned)((size_t)a.rope_rows * HD * 2));
+  const rsrc_t sinr = make_rsrc(a.sin_t, (unsigned)((size_t)a.rope_rows * HD * 2));
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
   const unsigned rec = ATT_REC;
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
@@ -854,9 +865,19 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       if (tk >= G && !(newest && pok)) continue;
       const int col = tk < G ? (kvh * G + tk) * HD : tk == G ? (NH + kvh) * HD : (NH + NKV + kvh) * HD;
       const unsigned ro = (unsigned)((size_t)b * nqkv + col) * 2;
+      // every load of the task is issued before the first use (one memory latency): raw head,
+      // norm weight, cos/sin row (row 0 stands in for an invalid position)
+      const rsrc_t wr = tk < G ? qwr : kwr_n;
+      const unsigned cb = (unsigned)((pok ? p0 : 0) * HD) * 2;
       float x0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rawr, ro + lane * 2, 0, 0));
       float x1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rawr, ro + (lane + 64) * 2, 0, 0));
-      if (tk <= G) head_norm_rope(a, x0, x1, tk < G ? qnw : knw, p0, pok, lane);
+      const float w0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(wr, lane * 2, 0, 0));
+      const float w1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(wr, (lane + 64) * 2, 0, 0));
+      const float c0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(cosr, cb + lane * 2, 0, 0));
+      const float c1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(cosr, cb + (lane + 64) * 2, 0, 0));
+      const float s0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(sinr, cb + lane * 2, 0, 0));
+      const float s1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(sinr, cb + (lane + 64) * 2, 0, 0));
+      if (tk <= G) head_norm_rope(a, x0, x1, w0, w1, c0, c1, s0, s1, pok);
       if (tk < G) {
         sh.u.a.qn[sg * G + tk][lane] = f2bf(x0);
         sh.u.a.qn[sg * G + tk][lane + 64] = f2bf(x1);
@@ -1062,10 +1083,10 @@ __device__ __forceinline__ bool phase_geo(const Args& a, const Shared& sh, int p
   const int kind = phase_kind(a, p, &layer);
   const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
   switch (kind) {
-    case P_QKV: *g = make_geo((const bf16*)lp[F_WQKV], (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV, true); return true;
-    case P_O:   *g = make_geo((const bf16*)lp[F_WO], a.H, a.NH * HD, LNR_O, false); return true;
-    case P_GU:  *g = make_geo((const bf16*)lp[F_WGU], 2 * a.I, a.H, LNR_GU, false); return true;
-    case P_D:   *g = make_geo((const bf16*)lp[F_WD], a.H, a.I, LNR_D, false); return true;
+    case P_QKV: *g = make_geo(uniform_ptr<const bf16>(lp[F_WQKV]), (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV, true); return true;
+    case P_O:   *g = make_geo(uniform_ptr<const bf16>(lp[F_WO]), a.H, a.NH * HD, LNR_O, false); return true;
+    case P_GU:  *g = make_geo(uniform_ptr<const bf16>(lp[F_WGU]), 2 * a.I, a.H, LNR_GU, false); return true;
+    case P_D:   *g = make_geo(uniform_ptr<const bf16>(lp[F_WD]), a.H, a.I, LNR_D, false); return true;
     case P_LM:  *g = make_geo(a.lm_t, a.V, a.H, LNR_LM, true); return true;
     default: return false;
   }
@@ -1232,7 +1253,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
     switch (kind) {
       case P_QKV:
         run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer),
-                                   (const bf16*)lp[F_LN1], ss_slot(a, 2 * layer));
+                                   uniform_ptr<const bf16>(lp[F_LN1]), ss_slot(a, 2 * layer));
         break;
       case P_O:
         run_gemv<LNR_O, EPI_RES, true>(a, sh, g, p, 2 * layer + 1, sync, epoch, a.NH * HD,
@@ -1240,7 +1261,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
         break;
       case P_GU:
         run_gemv<LNR_GU, EPI_SILU>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer + 1),
-                                   (const bf16*)lp[F_LN2], ss_slot(a, 2 * layer + 1));
+                                   uniform_ptr<const bf16>(lp[F_LN2]), ss_slot(a, 2 * layer + 1));
         break;
       case P_D:
         run_gemv<LNR_D, EPI_RES>(a, sh, g, p, 2 * layer + 2, sync, epoch, a.I, m_slot(a, layer),
@@ -1453,7 +1474,7 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   DD_REQUIRE(layer_table && embed && lm_tiled && final_norm && cos_t && sin_t && tok && pos);
   DD_REQUIRE(h && qkv && attn && mbuf && logits && ws && counters && err);
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, 0));
-  DD_REQUIRE(cap >= 1 && rope_rows >= 1);
+  DD_REQUIRE(cap >= 1 && rope_rows >= 1 && rope_rows <= (1 << 23));   // cos/sin byte ranges < 2^31
   DD_REQUIRE(phase_begin >= 0 && phase_begin < phase_end && phase_end <= 2 + 5 * L);
   int G = 0;
   const int e = step_grid(&G);
