@@ -356,17 +356,25 @@ __device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char
       }
     }
   };
+  // the sums of squares behind r are loaded first (one latency with the window): thread (q, m)
+  // takes groups q and q + 32 of row m (H / SSG <= 64), unconditionally (range-checked)
+  const int rm = t & (MAXM - 1), rq = t / MAXM;
+  float ss0 = 0.f, ss1 = 0.f;
+  if (lnw != nullptr) {
+    const rsrc_t ssr = make_rsrc(ss, (unsigned)(SS_SLOT * 4));
+    const int nq = a.H / SSG;
+    ss0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        ssr, rm < M && rq < nq ? (unsigned)((rq * MAXM + rm) * 4) : 0xfffffff0u, 0, 0));
+    ss1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        ssr, rm < M && rq + NTHR / MAXM < nq ? (unsigned)(((rq + NTHR / MAXM) * MAXM + rm) * 4)
+                                             : 0xfffffff0u, 0, 0));
+  }
   issue();
   // norm phases have K = H <= 64 * SSG (checked on the host): the window fits LNW_KS k-steps
   if (lnw != nullptr) {
     if (t < nw * 4) *(u32x4*)&sh.lnw[t * 8] = lwv;
-    // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): thread (p, m) sums groups p, p + 32, ...; then
-    // row m adds the 32 partials in order
-    const int m = t & (MAXM - 1), p = t / MAXM;
-    float s = 0.f;
-    if (m < M)
-      for (int q = p; q < a.H / SSG; q += NTHR / MAXM) s += ss[q * MAXM + m];
-    sh.rsp[p][m] = s;
+    // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): row m adds the 32 partials in order
+    sh.rsp[rq][rm] = ss0 + ss1;
     __syncthreads();
     if (t < M) {
       float r = 0.f;
