@@ -861,6 +861,35 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     __syncthreads();
     const int nsg = sh.nseg;
     const int inext = sh.segnext;
+    // one 32-key block of K (S^T operand: lane = key l16 of half t, dims kb*32 + g4*8) and V
+    // (rows of 16 keys x 8 dims, transposed through LDS below)
+    u32x4 kreg[2][4], vreg[8];
+    auto load_block = [&](size_t kvbase, int key0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        int key = key0 + t * 16 + l16;
+        key = key < a.cap ? key : a.cap - 1;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int cc = it * 64 + lane;
+        int key = key0 + (cc >> 4);
+        key = key < a.cap ? key : a.cap - 1;
+        vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
+      }
+    };
+    // the wave's first block of the round's first segment is loaded before the prologue, so its
+    // latency overlaps the prologue, unless it is the pair's newest block (whose key at pos the
+    // prologue writes)
+    bool pre = false;
+    if (nsg > 0) {
+      const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
+      const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
+      pre = wave < ns && j0 + wave != ((Lb + 31) >> 5) - 1;
+      if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
+    }
     // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; the
     // segment holding the newest block also writes K/V of position pos
     for (int task = wave; task < nsg * (G + 2); task += NWAVE) {
@@ -920,22 +949,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       bf16(*vs)[HD + 8] = sh.u.a.v[wave];
       for (int k = wave; k < nseg; k += NWAVE) {
         const int key0 = (j0 + k) * 32;
-        u32x4 kreg[2][4];
-        u32x4 vreg[8];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          int key = key0 + t * 16 + l16;
-          key = key < a.cap ? key : a.cap - 1;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
-        }
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-          const int cc = it * 64 + lane;
-          int key = key0 + (cc >> 4);
-          key = key < a.cap ? key : a.cap - 1;
-          vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
-        }
+        if (!(pre && sg == 0 && k == wave)) load_block(kvbase, key0);
         f32x4 sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
