@@ -883,7 +883,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     // the wave's first block of the round's first segment is loaded before the prologue, so its
     // latency overlaps the prologue, unless it is the pair's newest block (whose key at pos the
     // prologue writes)
-    bool pre = false;
+    bool pre = false;                        // kreg/vreg hold the wave's next block
     if (nsg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
       const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
@@ -949,7 +949,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       bf16(*vs)[HD + 8] = sh.u.a.v[wave];
       for (int k = wave; k < nseg; k += NWAVE) {
         const int key0 = (j0 + k) * 32;
-        if (!(pre && sg == 0 && k == wave)) load_block(kvbase, key0);
+        if (!pre) load_block(kvbase, key0);
         f32x4 sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -962,6 +962,17 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         for (int it = 0; it < 8; ++it) {
           const int cc = it * 64 + lane;
           *(u32x4*)&vs[cc >> 4][(cc & 15) * 8] = vreg[it];
+        }
+        // K and V of this block are consumed: the wave's next block (in this segment, else its
+        // first block of the next one) streams in during the softmax, P.V and merge
+        pre = false;
+        if (k + NWAVE < nseg) {
+          load_block(kvbase, key0 + NWAVE * 32);
+          pre = true;
+        } else if (sg + 1 < nsg && wave < sh.seg[sg + 1][3]) {
+          load_block((size_t)(sh.seg[sg + 1][0] * NKV + sh.seg[sg + 1][1]) * a.cap * HD,
+                     (sh.seg[sg + 1][2] + wave) * 32);
+          pre = true;
         }
         float sv[8];
         float mloc = -INFINITY;
