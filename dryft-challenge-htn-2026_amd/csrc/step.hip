@@ -41,7 +41,7 @@ constexpr int BATCH = 8;     // weight blocks (1 KB each) per prefetch batch per
 enum : int { F_WQKV = 0, F_WO, F_WGU, F_WD, F_LN1, F_LN2, F_QN, F_KN, F_KC, F_VC, NFIELD = 16 };
 
 // counters (ints)
-constexpr int C_BAR = 0;          // [0] top, [64 * (1 + xcd)] per XCD
+constexpr int C_BAR = 0;          // [64 * (1 + xcd)]: arrivals of the XCD's workgroups
 constexpr int C_EXIT = 640;
 constexpr int C_GROUP = 1024;     // per row-group fixup counters
 constexpr int C_ATT = C_GROUP + 8192;
@@ -262,25 +262,29 @@ struct GemvLds {
 __device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_s_barrier();
-  if (tid() == 0) {
-    const int xcd = blockIdx.x & 7;
-    const unsigned per = (unsigned)(gridDim.x >> 3);
-    const unsigned old = __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR + 64 * (1 + xcd), 1u,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == epoch * per - 1)
-      __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid() == 0)                            // no return value: nothing to wait for
+    __hip_atomic_fetch_add((unsigned*)a.ctr + C_BAR + 64 * (1 + (blockIdx.x & 7)), 1u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Released when every XCD's counter has all its workgroups' arrivals: lanes 0..7 of wave 0 read
+// the 8 counters in one load, so the release is one memory latency after the last arrival.
 __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epoch) {
-  if (tid() == 0 && !sh.bail) {
+  if (wave_id() == 0 && !sh.bail) {
+    const int lane = tid() & 63;
+    const unsigned target = epoch * (unsigned)(gridDim.x >> 3);
+    const rsrc_t cr = make_rsrc(a.ctr + C_BAR, 9 * 64 * 4);
+    const unsigned off = lane < 8 ? (unsigned)(64 * (1 + lane) * 4) : 0xfffffff0u;
     const unsigned long long t0 = wall_clock64();
-    while (__hip_atomic_load((unsigned*)a.ctr + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-           epoch * 8) {
+    for (;;) {
+      const unsigned v = ldc_u32(cr, off);
+      if (__all(lane >= 8 || v >= target)) break;
       __builtin_amdgcn_s_sleep(2);
       if (wall_clock64() - t0 > 20000000ull) {  // 200 ms: report, stop waiting from now on
-        atomicOr(a.err, E_TIMEOUT);
-        sh.bail = 1;
+        if (lane == 0) {
+          atomicOr(a.err, E_TIMEOUT);
+          sh.bail = 1;
+        }
         break;
       }
     }

@@ -71,7 +71,7 @@ def _step_args(**kw):
 @pytest.mark.parametrize("bad", [
     dict(M=17), dict(M=0), dict(NH=30), dict(cap=0), dict(rope_rows=0), dict(H=2500),
     dict(V=151930), dict(phase_end=3 + 5 * 36), dict(phase_begin=5, phase_end=5),
-    dict(tok=None), dict(counters=None), dict(NKV=64, NH=64),
+    dict(tok=None), dict(counters=None), dict(NKV=64, NH=64), dict(rope_rows=(1 << 23) + 1),
 ])
 def test_decode_step_validation(bad):
     """dd_decode_step checks shapes and pointers before it queries the device or launches."""
