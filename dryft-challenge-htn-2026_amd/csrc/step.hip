@@ -436,17 +436,27 @@ __device__ __forceinline__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], i
   }
 }
 
-__device__ __forceinline__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp, int hk) {
+// The residual input of the thread's two columns (thread t: row t / 32, columns 2 (t % 32) ..),
+// loaded when the group's flush starts so that its latency is off the finisher's chain.
+__device__ __forceinline__ unsigned epi_res_input(const Args& a, int grp, int hk) {
+  const int t = tid();
+  const int m = t >> 5, c2 = (t & 31) * 2;
+  const rsrc_t hin = make_rsrc(h_slot(a, hk - 1), (unsigned)((size_t)a.M * a.H * 2));
+  return __builtin_amdgcn_raw_buffer_load_b32(
+      hin, m < a.M ? (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2 : 0xfffffff0u, 0, 0);
+}
+
+__device__ __forceinline__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp, int hk,
+                                        unsigned hv2) {
   // 64 residual columns grp*64 .. : h[hk] = bf16(h[hk-1] + bf16(sum)); ss[hk][grp][m] = sum h^2
   const int M = a.M;
   const int t = tid();
   const int m = t >> 5, c2 = (t & 31) * 2;   // two columns per thread
   const unsigned bytes = (unsigned)((size_t)M * a.H * 2);
-  const rsrc_t hin = make_rsrc(h_slot(a, hk - 1), bytes), hout = make_rsrc(h_slot(a, hk), bytes);
+  const rsrc_t hout = make_rsrc(h_slot(a, hk), bytes);
   float q = 0.f;
   if (m < M) {
     const unsigned off = (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2;
-    const unsigned hv2 = __builtin_amdgcn_raw_buffer_load_b32(hin, off, 0, 0);
     const float h0 = rbf(lo_bf(hv2) + rbf(res[c2][m]));
     const float h1 = rbf(hi_bf(hv2) + rbf(res[c2 + 1][m]));
     stc_u32(hout, off, (unsigned)f2bf(h0) | ((unsigned)f2bf(h1) << 16));
@@ -509,9 +519,9 @@ __device__ __forceinline__ void epi_logits(const Args& a, Shared& sh, float (*re
 // Run the epilogue of a row group whose fp32 sums are in res.
 template <int EPI>
 __device__ __forceinline__ void run_epilogue(const Args& a, Shared& sh, float (*res)[MAXM + 1],
-                                             int grp, int layer) {
+                                             int grp, int layer, unsigned hres) {
   if (EPI == EPI_QKV) epi_qkv(a, res, layer, grp);
-  else if (EPI == EPI_RES) epi_res(a, res, grp, layer);   // layer: output h slot
+  else if (EPI == EPI_RES) epi_res(a, res, grp, layer, hres);   // layer: output h slot
   else if (EPI == EPI_SILU) epi_silu(a, res, grp, layer);
   else epi_logits(a, sh, res, grp);
 }
@@ -526,6 +536,7 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
   const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
   GemvLds<NR> L(sh);
+  const unsigned hres = EPI == EPI_RES ? epi_res_input(a, grp, layer) : 0u;
 #pragma unroll
   for (int t = 0; t < NR; ++t) {
 #pragma unroll
@@ -603,7 +614,7 @@ __device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo
       STEP_TRACE(p, 6);
     }
   }
-  if (finish) run_epilogue<EPI>(a, sh, L.res, grp, layer);
+  if (finish) run_epilogue<EPI>(a, sh, L.res, grp, layer, hres);
   if (finish && first != last) STEP_TRACE(p, 7);
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
