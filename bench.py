@@ -58,6 +58,22 @@ def measure_read_bw(torch, L, nbytes=4 << 30):
     return best
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_step_kernel_b16_configs4_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the step kernel from the committed rocprofv3 --pmc runs of this
+    same workload (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel calibration);
+    None when the file is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    scale = t["copy_calibration"]["scale"] * 1024
+    return int((t["fetch_kib_per_dispatch"] + t["write_kib_per_dispatch"]) * scale)
+
+
 def step_roofline(ms, bytes_step, B):
     """The dominant (and only) kernel of a decode step is the one-launch step kernel: the timed
     region is K graph replays of one launch each, timed with HIP events on the stream they run
@@ -68,7 +84,8 @@ def step_roofline(ms, bytes_step, B):
     return {"kernel": "dd::st::decode_step_kernel (whole decode step, one launch)",
             "bound": "hbm", "achieved": round(bytes_step / avg_s / 1e9, 1),
             "peak": SPEC_BW / 1e9, "unit": "GB/s", "frac": round(bytes_step / avg_s / SPEC_BW, 4),
-            "traffic": None, "avg_launch_us": round(avg_s * 1e6, 2),
+            "traffic": measured_traffic() if B == 16 else None,
+            "avg_launch_us": round(avg_s * 1e6, 2),
             "algo_bytes_per_launch": int(bytes_step), "rows": B}
 
 
