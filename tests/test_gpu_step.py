@@ -164,6 +164,21 @@ def test_fused_step_qwen3_width_b16(cuda):
     print(f"qwen3-width B=16: worst logit diff {worst:.4f}, near-tie flips {flips}")
 
 
+@pytest.mark.parametrize("B,lo,hi", [(16, 512, 8192), (1, 7000, 8000)])
+def test_fused_step_long_context(cuda, B, lo, hi):
+    """configs[2]'s context range (ragged 512-8192 keys, cache capacity ~8192) through the fused
+    step at Qwen3-4B widths (one layer): at B=16 every (row, kv head) is split over several
+    attention workgroups; at B=1 each of the 8 is split over ~17, past the O staging's fast path
+    of 3 contributors."""
+    cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
+    ref, eng = _engine(cfg, seed=21)
+    g = torch.Generator().manual_seed(22)
+    lens = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
+    prompts = [torch.randint(0, 8192, (L,), generator=g).tolist() for L in lens]
+    worst, flips = _step_parity(ref, eng, prompts, 1, seed=23)
+    print(f"long context B={B}: worst logit diff {worst:.4f}, near-tie flips {flips}")
+
+
 def _close(got, want, what, rtol=2e-2, atol=2e-2):
     got, want = got.float(), want.float()
     d = (got - want).abs()
