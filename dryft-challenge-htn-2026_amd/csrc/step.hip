@@ -1,31 +1,32 @@
 // Persistent decode step for MI355X (gfx950): one launch runs a whole Qwen3-shape decode step.
 //
 // Grid: one 512-thread workgroup per CU, all co-resident. The step is a fixed list of phases:
-//   0            embedding gather  h = embed[tok], per-64-column sums of squares
-//   per layer    QKV GEMV (+ per-head q/k RMSNorm, RoPE, K/V cache write)
-//                split-KV attention (+ log-sum-exp combine)
+//   0            embedding gather  h = embed[tok], per-workgroup sums of squares
+//   per layer    QKV GEMV (raw q|k|v)
+//                attention (q/k RMSNorm + RoPE + K/V cache write, split-KV, log-sum-exp combine)
 //                O GEMV (+ residual, sums of squares)
 //                gate/up GEMV (+ SiLU x up)
 //                down GEMV (+ residual, sums of squares)
 //   last         lm_head GEMV (+ logits, argmax, pos += 1)
 // with a grid barrier between phases.
 //
-// GEMV phases stream weights that were re-laid out once into "MFMA tile order" (dd_tile_weight):
-// the A operand of one v_mfma_f32_16x16x32_bf16 (16 rows x 32 k) is one contiguous 1 KB block
-// in lane order, so every weight load instruction of a wave reads 1 KB contiguous (a 16-row x
-// 64-byte pattern only reaches ~70% of the HBM bandwidth on MI355X). NR tiles that share a group
-// of rows sit next to each other per 32-k step ("step" = NR blocks). Each workgroup owns a
-// contiguous range of steps (stream-K): equal bytes per CU; a row group cut between workgroups
-// is finished by the last of its contributors to arrive (partials in split order: deterministic).
-// The activation operand x of a phase is staged once into LDS per workgroup (only the k window
-// that workgroup needs), with the RMSNorm of the residual stream applied on the way in.
+// GEMV phases: every workgroup owns whole output rows over the whole K (rows split evenly over
+// the workgroups: 10 rows of O/down, 24 of QKV, 38 gate+up feature pairs, ~594 vocabulary rows
+// at Qwen3-4B widths on 256 CUs), so no output is ever split between workgroups: no partial
+// sums, no finishing hand-offs, each workgroup runs its own epilogue. A workgroup's rows are
+// processed in chunks of up to T 16-row MFMA tiles; its 8 waves split the 32-column k-steps
+// (wave w takes k-steps w, w + 8, ...) and meet once per chunk in LDS. Weights are streamed from
+// a copy re-laid out once (dd_tile_weight): per workgroup and chunk, k-step-major, so one wave
+// load of a tile reads rows x 64 contiguous bytes. The activation operand (16 rows x K) is loaded
+// by each wave straight into MFMA B-operand registers from the L2 (each XCD's L2 fetches it
+// once), RMS-normalised in registers where the phase takes a normalised input.
 //
 // Barriers are split: a workgroup arrives (after its stores completed), then issues the weight
 // loads of the next phase, then waits -- the HBM stream keeps going through the barrier.
 //
-// Cross-workgroup data inside the launch moves with sc1 stores/loads (served at the device
-// coherence point, see common.h); every spin has a wall-clock timeout that raises a flag
-// instead of hanging.
+// Cross-workgroup data inside the launch moves with sc1 stores (written through to the device
+// coherence point, see common.h); every spin has a wall-clock timeout that raises a flag instead
+// of hanging.
 #include "common.h"
 
 namespace dd {
@@ -34,25 +35,38 @@ namespace st {
 constexpr int NWAVE = 8;
 constexpr int NTHR = NWAVE * 64;
 constexpr int HD = 128;
-constexpr int SSG = 64;      // residual columns per sum-of-squares group (O/down row group)
 constexpr int MAXM = 16;
-constexpr int BATCH = 8;     // weight blocks (1 KB each) per prefetch batch per wave
+constexpr unsigned OOB = 0x80000000u;   // buffer offset past every range: the load reads 0
+#ifndef DD_BAR_SLEEP
+#define DD_BAR_SLEEP 2       // s_sleep between barrier polls (units of 64 cycles)
+#endif
 
 enum : int { F_WQKV = 0, F_WO, F_WGU, F_WD, F_LN1, F_LN2, F_QN, F_KN, F_KC, F_VC, NFIELD = 16 };
 
 // counters (ints)
 constexpr int C_BAR = 0;          // [64 * (1 + xcd)]: arrivals of the XCD's workgroups
 constexpr int C_EXIT = 640;
-constexpr int C_GROUP = 1024;     // per row-group fixup counters
-constexpr int C_ATT = C_GROUP + 8192;
+constexpr int C_ATT = 1024;       // per (row, kv head) attention combine counters
 constexpr int C_AM = C_ATT + 512;
 constexpr int C_TOTAL = C_AM + 64;
 
 // error flags
 constexpr int E_TOKEN = 1, E_POS = 2, E_TIMEOUT = 4, E_GEOM = 8;
 
-// tiles per row group of each GEMV phase (log2)
-constexpr int LNR_QKV = 1, LNR_O = 2, LNR_GU = 1, LNR_D = 2, LNR_LM = 1;
+// The GEMV matrices and their per-workgroup layout: T tiles (16 rows each) per chunk, KB k-steps
+// per prefetch batch, UPR weight rows per unit of the partition (gate/up: one unit = one feature
+// = its gate row and its up row, kept in the same chunk for the SiLU epilogue).
+enum : int { M_QKV = 0, M_O = 1, M_GU = 2, M_D = 3, M_LM = 4, NMAT = 5 };
+__host__ __device__ constexpr int mat_T(int k) { return k == M_QKV ? 2 : k == M_GU ? 5 : k == M_LM ? 8 : 1; }
+__host__ __device__ constexpr int mat_KB(int k) { return k == M_QKV ? 4 : k == M_GU ? 2 : k == M_LM ? 1 : 8; }
+__host__ __device__ constexpr int mat_UPR(int k) { return k == M_GU ? 2 : 1; }
+__host__ __device__ constexpr int mat_CAPU(int k) { return mat_T(k) * 16 / mat_UPR(k); }
+constexpr int TMAX = 8;
+
+// first unit of workgroup c when n units are split evenly over G workgroups (n * G < 2^32)
+__host__ __device__ inline int part_lo(int n, int G, int c) {
+  return (int)(((unsigned)n * (unsigned)c) / (unsigned)G);
+}
 
 // Thread index read through an opaque move: values derived from it cannot be hoisted out of
 // the phase that computes them, so they do not stay live (in registers or spilled) across the
@@ -95,7 +109,7 @@ __device__ unsigned long long g_trace[1024 * TR_PHASES * TR_EVENTS];
 struct Args {
   const int64_t* layers;             // [L][NFIELD] device pointers
   const bf16* embed;                 // [V][H] natural layout (gather)
-  const bf16* lm_t;                  // lm_head, tiled with NR = 2
+  const bf16* lm_t;                  // lm_head, tiled (M_LM)
   const bf16* fnorm;                 // final RMSNorm weight [H]
   const bf16* cos_t;
   const bf16* sin_t;
@@ -112,52 +126,21 @@ struct Args {
   int L, M, H, NH, NKV, I, V, cap, rope_rows;
   float eps;
   int phase_begin, phase_end;
-  unsigned off_ss, off_part, off_att, off_am;   // workspace offsets (floats); ss: [2L+1][64][16]
-  unsigned ws_floats;
+  unsigned off_ss, off_att, off_am;  // workspace offsets (floats); ss: [2L+1][G][16]
 };
-
-// The steps of a phase are split into equal contiguous workgroup ranges in units of `unit`
-// steps: 1 (stream-K: equal bytes per workgroup; a row group cut between workgroups is finished
-// by its last contributor) or nk (whole row groups per workgroup: no cross-workgroup partials,
-// balanced when there are many groups per workgroup or the epilogue needs the whole group).
-struct Geo {                         // one GEMV phase for this workgroup
-  const bf16* W;
-  rsrc_t wr;                         // this workgroup's steps s0 .. s1 of W (range-checked)
-  int lnr, nk, ngroups, S, unit, nu, s0, s1;
-};
-
-__device__ __forceinline__ Geo make_geo(const bf16* W, int rows, int K, int lnr, bool whole) {
-  Geo g;
-  g.W = W;
-  g.lnr = lnr;
-  g.nk = K >> 5;
-  g.ngroups = rows >> (4 + lnr);
-  g.S = g.ngroups * g.nk;
-  g.unit = whole ? g.nk : 1;
-  g.nu = whole ? g.ngroups : g.S;
-  g.s0 = (int)((unsigned)g.nu * blockIdx.x / gridDim.x) * g.unit;
-  g.s1 = (int)((unsigned)g.nu * (blockIdx.x + 1) / gridDim.x) * g.unit;
-  g.wr = make_rsrc(W + ((size_t)g.s0 << (9 + lnr)), (unsigned)((g.s1 - g.s0) << (10 + lnr)));
-  return g;
-}
-
-// workgroup owning global step s
-__device__ __forceinline__ int wg_of_step(const Geo& g, int s) {
-  return (int)(((unsigned)(s / g.unit + 1) * gridDim.x - 1) / (unsigned)g.nu);
-}
 
 // Activation buffers are write-once within a launch: the residual stream h has one slot per
 // phase that produces it (embedding -> 0, O of layer l -> 2l+1, down of layer l -> 2l+2), raw
-// q|k|v, attention output and SiLU output one slot per layer. A slot is only read after the phase that
-// writes it (through to the device coherence point, sc1) and every cache is clean at launch
+// q|k|v, attention output and SiLU output one slot per layer. A slot is only read after the phase
+// that writes it (through to the device coherence point, sc1) and every cache is clean at launch
 // start, so no cache can hold a stale copy: readers use plain cached loads, and each XCD's L2
-// fetches a line once for all its workgroups.
-constexpr int SS_SLOT = 64 * MAXM;   // floats per sums-of-squares slot ([H/64 <= 64][16])
+// fetches a line once for all its workgroups. The sums of squares behind the RMSNorms follow the
+// same rule: slot k holds one [16] partial per workgroup (its columns of h slot k).
 __device__ __forceinline__ bf16* h_slot(const Args& a, int k) {
   return a.h + (size_t)k * a.M * a.H;
 }
 __device__ __forceinline__ float* ss_slot(const Args& a, int k) {
-  return a.ws + a.off_ss + (size_t)k * SS_SLOT;
+  return a.ws + a.off_ss + (size_t)k * gridDim.x * MAXM;
 }
 __device__ __forceinline__ bf16* qkv_slot(const Args& a, int l) {
   return a.qkv + (size_t)l * a.M * (a.NH + 2 * a.NKV) * HD;
@@ -169,69 +152,43 @@ __device__ __forceinline__ bf16* m_slot(const Args& a, int l) {
   return a.mbuf + (size_t)l * a.M * a.I;
 }
 // split-attention partials of a layer ([G][2][heads per kv head][ATT_REC] fp32): write-once
+constexpr int ATT_REC = HD + 4;      // o[128], m, l, 2 pad (16-byte rows)
 __device__ __forceinline__ float* att_part(const Args& a, int l) {
-  return a.ws + a.off_att + (size_t)l * gridDim.x * 2 * (a.NH / a.NKV) * (HD + 4);
+  return a.ws + a.off_att + (size_t)l * gridDim.x * 2 * (a.NH / a.NKV) * ATT_REC;
 }
 // plain (cached) 16-byte buffer load; out-of-range offsets read zeros
 __device__ __forceinline__ u32x4 ldb128(rsrc_t r, unsigned off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
-
-// first step of workgroup c's range (ranges of workgroups between two owners may be empty)
-__device__ __forceinline__ int step0_of(const Geo& g, int c) {
-  return (int)((unsigned)g.nu * c / gridDim.x) * g.unit;
-}
-
-// Issue the wave's weight loads for wave-step index j0 .. (a batch of BATCH blocks). The loads
-// are unconditional buffer loads through the workgroup's range descriptor: a step past the
-// range reads zeros without touching memory, and with no branches around the loads the compiler
-// waits for each buffer register on its own (vmcnt(n)) instead of draining the queue. The whole
-// offset is in the VGPR operand: the SGPR offset is not range-checked.
 constexpr int CP_NT = 2;   // buffer cache-policy bit nt (streaming)
 
-template <int NR>
-__device__ __forceinline__ void issue_batch(const Geo& g, int j0, u32x4 (&buf)[BATCH]) {
-  const int lane = tid() & 63, wave = wave_id();
-#pragma unroll
-  for (int b = 0; b < BATCH; ++b) {
-    const int u = b / NR, t = b % NR;
-    const int sl = wave + NWAVE * (j0 + u);          // step relative to s0
-    buf[b] = __builtin_amdgcn_raw_buffer_load_b128(g.wr, lane * 16 + ((sl * NR + t) << 10), 0,
-                                                   CP_NT);
-  }
-}
-
-// GEMV phases carve their LDS out of one region: per-wave partial tiles (NR x 8 KB), the
-// reduced group tile, then the staged activation window.
-constexpr int GBUF = 112 * 1024;
-constexpr int RES_BYTES = 8 * 16 * (MAXM + 1) * 4;
-__host__ __device__ constexpr int x_capacity(int NR) { return GBUF - NR * NWAVE * 256 * 4 - RES_BYTES; }
-
-constexpr int LNW_KS = 128;                   // k-steps of the norm weight staged in LDS
 constexpr int MAXG = 512;                     // workgroups (CUs) the step kernel supports
 constexpr int MAXG_HEADS = 8;                 // query heads per kv head
 constexpr int MAXL = 64;                      // layers
 constexpr int LFIELDS = 10;                   // layer-table fields the phases read
+constexpr int MAXH = 4096;                    // hidden size (norm weight staged in LDS)
 
 struct Shared {
   union {
-    unsigned char g[GBUF];                    // GEMV phases (see GemvLds)
+    struct {                                  // GEMV phases
+      float red[NWAVE][TMAX][256];            // per-wave partial tiles of a chunk
+      float res[TMAX * 16][MAXM + 1];         // the chunk's reduced rows
+    } g;
     struct {                                  // attention
       bf16 v[NWAVE][32][HD + 8];
       float mrg[NWAVE][MAXG_HEADS][HD];
       bf16 qn[32][HD];                        // normalised, rotated query heads of the segments
     } a;
   } u;
-  float rs[MAXM];                             // per-row 1/rms of the staged x
-  float rsp[NTHR / MAXM][MAXM];               // partial sums of squares behind rs
+  bf16 lnw[MAXH];                             // norm weight of a normalised-input GEMV phase
+  float rs[MAXM];                             // per-row 1/rms of the phase's input
+  float rsp[NWAVE][MAXM];                     // per-wave partial sums of squares behind rs
   float ms[NWAVE][16];
   float ls[NWAVE][16];
   float bestv[MAXM];
   int besti[MAXM];
   int flag;
   int bail;                                   // a barrier wait timed out: stop waiting
-  int xrs;                                    // staged x row stride (bytes)
-  int xksf, xnw;                              // staged window: first k-step, width
   int units[MAXM + 1];                        // attention unit prefix sums
   int seg[32][4];                             // attention segments: b, kvh, first block, blocks
   int nseg, segnext;
@@ -239,25 +196,17 @@ struct Shared {
   int afirst[MAXG + 1];                       // attention: first unit of each workgroup
   int aG;                                     // attention: workgroups holding units
   long long ltab[MAXL][LFIELDS];              // the layer table, copied once per launch
-  int pinfo[MAXM * 32][8];                    // O staging: per (row, kv head) fw, lw, record
-                                              // offsets of its first 3 contributors (-1: none), S
-  bf16 lnw[LNW_KS * 32];                      // staged norm weight window (<= LNW_KS k-steps)
 };
 
 static_assert(sizeof(Shared) <= 160 * 1024, "LDS budget of one CU");
 
-// ---------------------------------------------------------------------------------------------
-template <int NR>
-struct GemvLds {
-  float (*red)[NR][256];                      // [NWAVE][NR][256]
-  float (*res)[MAXM + 1];                     // [NR*16][MAXM+1]
-  unsigned char* x;
-  __device__ explicit GemvLds(Shared& sh)
-      : red((float(*)[NR][256])sh.u.g),
-        res((float(*)[MAXM + 1])(sh.u.g + NR * NWAVE * 256 * 4)),
-        x(sh.u.g + NR * NWAVE * 256 * 4 + RES_BYTES) {}
-};
+// LDS-only wait + workgroup barrier (outstanding global loads are not waited for)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
 
+// ---------------------------------------------------------------------------------------------
 // barrier (split)
 __device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
   __builtin_amdgcn_s_waitcnt(0);
@@ -279,7 +228,7 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
     for (;;) {
       const unsigned v = ldc_u32(cr, off);
       if (__all(lane >= 8 || v >= target)) break;
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(DD_BAR_SLEEP);
       if (wall_clock64() - t0 > 20000000ull) {  // 200 ms: report, stop waiting from now on
         if (lane == 0) {
           atomicOr(a.err, E_TIMEOUT);
@@ -293,196 +242,119 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
 }
 
 // ---------------------------------------------------------------------------------------------
-// activation staging: x window [ksf, ksf + nw) (cyclic over nk k-steps) of an [M][K] source into
-// LDS rows of stride xrs bytes. NORM: x = bf16(bf16(h * r[m]) * lnw[k]) with r from the ss groups.
-// Every load of a batch is issued before the first is used (one memory latency per batch of
-// SBATCH items per thread), and the first batch is in flight while r is reduced. The norm
-// weight window (the same for every row) is staged once into LDS.
-constexpr int SBATCH = 12;
+// GEMV phases
 
-__device__ __forceinline__ unsigned stage_off(int it, int nw, int ksf, int nk, int K, int* lds) {
-  const int m = it / (nw * 4);
-  const int rem = it - m * nw * 4;
-  const int w = rem >> 2, e = rem & 3;
-  int ks = ksf + w;
-  if (ks >= nk) ks -= nk;
-  *lds = w * 64 + e * 16;
-  return (unsigned)((size_t)m * K + ks * 32 + e * 8);
+// This workgroup's share of one GEMV phase: units u0 .. u0 + nu of the matrix, nch chunks of up
+// to CAPU units, nbpc prefetch batches per chunk (every wave has nk / 8 k-steps), nb batches.
+struct Geo {
+  rsrc_t wr;                         // the workgroup's weight region (all its chunks)
+  int K, nk, u0, nu, nch, nbpc, nb;
+};
+
+template <int KIND>
+__device__ __forceinline__ Geo make_geo(const bf16* W, int nunits, int K) {
+  constexpr int UPR = mat_UPR(KIND), CAPU = mat_CAPU(KIND), KB = mat_KB(KIND);
+  Geo g;
+  g.K = K;
+  g.nk = K >> 5;
+  const int u0 = part_lo(nunits, gridDim.x, blockIdx.x);
+  const int u1 = part_lo(nunits, gridDim.x, blockIdx.x + 1);
+  g.u0 = u0;
+  g.nu = u1 - u0;
+  g.nch = (g.nu + CAPU - 1) / CAPU;
+  g.nbpc = ((g.nk >> 3) + KB - 1) / KB;
+  g.nb = g.nch * g.nbpc;
+  g.wr = make_rsrc(W + (size_t)u0 * UPR * K, (unsigned)((size_t)g.nu * UPR * K * 2));
+  return g;
 }
 
-// The norm weight of the window does not depend on the previous phase: its load is issued before
-// the barrier wait (thread t < 4 * window holds 16 bytes of k-step t / 4).
-__device__ __forceinline__ u32x4 lnw_prefetch(const Geo& g, const bf16* lnw, int K) {
-  const int t = tid();
-  const int ksf = g.s1 > g.s0 ? g.s0 % g.nk : 0;
-  const int nw = g.s1 > g.s0 ? min(g.s1 - g.s0, g.nk) : 0;
-  int ks = ksf + (t >> 2);
-  if (ks >= g.nk) ks -= g.nk;
-  const rsrc_t r = make_rsrc(lnw, (unsigned)(K * 2));
-  return ldb128(r, t < nw * 4 ? (unsigned)((ks * 32 + (t & 3) * 8) * 2) : 0xfffffff0u);
+// weight rows of chunk ch
+template <int KIND>
+__device__ __forceinline__ int chunk_rows(const Geo& g, int ch) {
+  return min(mat_CAPU(KIND), g.nu - ch * mat_CAPU(KIND)) * mat_UPR(KIND);
 }
 
-__device__ __forceinline__ void stage_x(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
-                                        int K, const bf16* src, const bf16* lnw, u32x4 lwv,
-                                        const float* ss, int p) {
-  const int M = a.M;
-  const int t = tid();
-  int ksf = 0, nw = 0;
-  if (g.s1 > g.s0) {
-    ksf = g.s0 % g.nk;
-    nw = min(g.s1 - g.s0, g.nk);
-  }
-  const int xrs = nw * 64 + 16;
-  const int W = nw * 4;                       // 16-byte items per row
-  const int items = M * W;
-  const rsrc_t sr = make_rsrc(src, (unsigned)((size_t)M * K * 2));
-  // thread t takes items t, t + NTHR, ... (item = m * W + r); (m, r) advance without dividing
-  const int Wd = W > 0 ? W : 1;
-  const int dq = NTHR / Wd, dr = NTHR - dq * Wd;
-  int cm = t / Wd, cr = t - (t / Wd) * Wd;    // the thread's next item
-  u32x4 v[SBATCH];
-  int lo_[SBATCH], m_[SBATCH];                // LDS byte offset within the row, row (-1: none)
-  auto issue = [&]() {
+// One prefetch batch of a wave: KB k-steps, each T weight tiles (MFMA A operands) and the
+// activation block (B operand: lane l = row l % 16, columns (l / 16) * 8 .. +8 of the k-step).
+template <int KIND>
+struct Buf {
+  u32x4 w[mat_KB(KIND)][mat_T(KIND)];
+  u32x4 x[mat_KB(KIND)];
+};
+
+// Weight loads of batch bi (chunk bi / nbpc). Loads are unconditional buffer loads: a tile row
+// past the chunk, a k-step past K or a batch past the workgroup's share reads zeros without
+// memory traffic, so the compiler waits for each register on its own (vmcnt(n)).
+template <int KIND>
+__device__ __forceinline__ void issue_w(const Geo& g, int bi, Buf<KIND>& b) {
+  constexpr int T = mat_T(KIND), KB = mat_KB(KIND), CAPU = mat_CAPU(KIND), UPR = mat_UPR(KIND);
+  const int lane = tid() & 63, wave = wave_id();
+  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
+  const bool chok = ch < g.nch;
+  const int rows = chok ? chunk_rows<KIND>(g, ch) : 0;
+  const unsigned cbase = (unsigned)(ch * CAPU * UPR) * (unsigned)g.K * 2u;
 #pragma unroll
-    for (int b = 0; b < SBATCH; ++b) {
-      const bool ok = cm < M;
-      const int w = cr >> 2, e = cr & 3;
-      int ks = ksf + w;
-      if (ks >= g.nk) ks -= g.nk;
-      lo_[b] = w * 64 + e * 16;
-      m_[b] = ok ? cm : -1;
-      v[b] = ldb128(sr, ok ? (unsigned)((cm * K + ks * 32 + e * 8) * 2) : 0xfffffff0u);
-      cr += dr;
-      cm += dq;
-      if (cr >= Wd) {
-        cr -= Wd;
-        ++cm;
-      }
-    }
-  };
-  // the sums of squares behind r are loaded first (one latency with the window): thread (q, m)
-  // takes groups q and q + 32 of row m (H / SSG <= 64), unconditionally (range-checked)
-  const int rm = t & (MAXM - 1), rq = t / MAXM;
-  float ss0 = 0.f, ss1 = 0.f;
-  if (lnw != nullptr) {
-    const rsrc_t ssr = make_rsrc(ss, (unsigned)(SS_SLOT * 4));
-    const int nq = a.H / SSG;
-    ss0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        ssr, rm < M && rq < nq ? (unsigned)((rq * MAXM + rm) * 4) : 0xfffffff0u, 0, 0));
-    ss1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        ssr, rm < M && rq + NTHR / MAXM < nq ? (unsigned)(((rq + NTHR / MAXM) * MAXM + rm) * 4)
-                                             : 0xfffffff0u, 0, 0));
-  }
-  issue();
-  // norm phases have K = H <= 64 * SSG (checked on the host): the window fits LNW_KS k-steps
-  if (lnw != nullptr) {
-    if (t < nw * 4) *(u32x4*)&sh.lnw[t * 8] = lwv;
-    // r[m] = 1/sqrt(sum_q ss[q][m] / H + eps): row m adds the 32 partials in order
-    sh.rsp[rq][rm] = ss0 + ss1;
-    __syncthreads();
-    if (t < M) {
-      float r = 0.f;
-#pragma unroll 8
-      for (int q = 0; q < NTHR / MAXM; ++q) r += sh.rsp[q][t];
-      sh.rs[t] = rsqrt_ieee(r / (float)a.H + a.eps);
+  for (int kb = 0; kb < KB; ++kb) {
+    const int ks = wave + NWAVE * (bb * KB + kb);
+    const bool okk = chok && ks < g.nk;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int j = 16 * t + (lane & 15);
+      const bool ok = okk && j < rows;
+      b.w[kb][t] = __builtin_amdgcn_raw_buffer_load_b128(
+          g.wr, ok ? cbase + (unsigned)(ks * rows + j) * 64u + (unsigned)(lane >> 4) * 16u : OOB, 0,
+          CP_NT);
     }
   }
-  STEP_TRACE(p, 8);
-  if (t == 0) {
-    sh.xrs = xrs;
-    sh.xksf = ksf;
-    sh.xnw = nw;
-  }
-  __syncthreads();
-  for (int base = 0; base < items; base += SBATCH * NTHR) {
-    if (base > 0) issue();
-#pragma unroll
-    for (int b = 0; b < SBATCH; ++b) {
-      const int m = m_[b];
-      if (m < 0) break;
-      u32x4 x = v[b];
-      if (lnw != nullptr) {
-        const float r = sh.rs[m];
-        const u32x4 wv = *(const u32x4*)&sh.lnw[(lo_[b] >> 4) * 8];
-        const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
-        unsigned o[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          o[j] = pk_bf16(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]), rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
-        x = u32x4{o[0], o[1], o[2], o[3]};
-      }
-      *(u32x4*)(xb + m * xrs + lo_[b]) = x;
-    }
-  }
-  STEP_TRACE(p, 9);
-  __syncthreads();
 }
 
-// ---------------------------------------------------------------------------------------------
-// GEMV epilogues. `res[row][m]` holds the fp32 sums of the group's NR*16 weight rows.
+template <int KIND>
+__device__ __forceinline__ void issue_x(const Geo& g, rsrc_t xr, int M, int bi, Buf<KIND>& b) {
+  constexpr int KB = mat_KB(KIND);
+  const int lane = tid() & 63, wave = wave_id();
+  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
+  const bool chok = ch < g.nch && (lane & 15) < M;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int ks = wave + NWAVE * (bb * KB + kb);
+    const bool ok = chok && ks < g.nk;
+    b.x[kb] = ldb128(xr, ok ? (unsigned)(((lane & 15) * g.K + ks * 32 + (lane >> 4) * 8) * 2) : OOB);
+  }
+}
+
+// x = bf16(bf16(h * r) * w) for the 8 values of one B-operand register
+__device__ __forceinline__ u32x4 norm8(u32x4 x, float r, u32x4 wv) {
+  const unsigned hw[4] = {x.x, x.y, x.z, x.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  unsigned o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = pk_bf16(rbf(lo_bf(hw[j]) * r) * lo_bf(ww[j]), rbf(hi_bf(hw[j]) * r) * hi_bf(ww[j]));
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <int KIND, bool NORM>
+__device__ __forceinline__ void consume(const Geo& g, const Shared& sh, const Buf<KIND>& b, int bi,
+                                        float r, f32x4 (&acc)[mat_T(KIND)]) {
+  constexpr int T = mat_T(KIND), KB = mat_KB(KIND);
+  const int lane = tid() & 63, wave = wave_id();
+  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
+  if (ch >= g.nch) return;
+  const int rows = chunk_rows<KIND>(g, ch);
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    u32x4 xv = b.x[kb];
+    if (NORM) {
+      const int ks = min(wave + NWAVE * (bb * KB + kb), g.nk - 1);
+      xv = norm8(xv, r, *(const u32x4*)&sh.lnw[ks * 32 + (lane >> 4) * 8]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (16 * t < rows) acc[t] = mfma16x16x32(b.w[kb][t], xv, acc[t]);
+  }
+}
+
+// epilogues: `res[row][m]` holds the fp32 sums of the chunk's weight rows
 enum { EPI_QKV = 0, EPI_RES = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
-
-__device__ __forceinline__ void epi_qkv(const Args& a, float (*res)[MAXM + 1], int layer, int grp) {
-  // raw q|k|v rows grp*32 .. +32 for every token (q/k RMSNorm, RoPE and the K/V cache write
-  // happen in the attention phase, which holds whole heads)
-  constexpr int ROWS = 16 << LNR_QKV;
-  const int M = a.M;
-  const int t = tid();
-  const int r = t % ROWS, m = t / ROWS;
-  const int nqkv = (a.NH + 2 * a.NKV) * HD;
-  if (m < M) {
-    const rsrc_t qr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
-    stc_b16(qr, (unsigned)((size_t)m * nqkv + grp * ROWS + r) * 2, f2bf(res[r][m]));
-  }
-}
-
-// The residual input of the thread's two columns (thread t: row t / 32, columns 2 (t % 32) ..),
-// loaded when the group's flush starts so that its latency is off the finisher's chain.
-__device__ __forceinline__ unsigned epi_res_input(const Args& a, int grp, int hk) {
-  const int t = tid();
-  const int m = t >> 5, c2 = (t & 31) * 2;
-  const rsrc_t hin = make_rsrc(h_slot(a, hk - 1), (unsigned)((size_t)a.M * a.H * 2));
-  return __builtin_amdgcn_raw_buffer_load_b32(
-      hin, m < a.M ? (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2 : 0xfffffff0u, 0, 0);
-}
-
-__device__ __forceinline__ void epi_res(const Args& a, float (*res)[MAXM + 1], int grp, int hk,
-                                        unsigned hv2) {
-  // 64 residual columns grp*64 .. : h[hk] = bf16(h[hk-1] + bf16(sum)); ss[hk][grp][m] = sum h^2
-  const int M = a.M;
-  const int t = tid();
-  const int m = t >> 5, c2 = (t & 31) * 2;   // two columns per thread
-  const unsigned bytes = (unsigned)((size_t)M * a.H * 2);
-  const rsrc_t hout = make_rsrc(h_slot(a, hk), bytes);
-  float q = 0.f;
-  if (m < M) {
-    const unsigned off = (unsigned)((size_t)m * a.H + grp * SSG + c2) * 2;
-    const float h0 = rbf(lo_bf(hv2) + rbf(res[c2][m]));
-    const float h1 = rbf(hi_bf(hv2) + rbf(res[c2 + 1][m]));
-    stc_u32(hout, off, (unsigned)f2bf(h0) | ((unsigned)f2bf(h1) << 16));
-    q = h0 * h0 + h1 * h1;
-  }
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
-  if (m < M && (t & 31) == 0) {
-    const rsrc_t ssr = make_rsrc(ss_slot(a, hk), (unsigned)(SS_SLOT * 4));
-    stc_f32(ssr, (unsigned)(grp * MAXM + m) * 4, q);
-  }
-}
-
-__device__ __forceinline__ void epi_silu(const Args& a, float (*res)[MAXM + 1], int grp, int layer) {
-  // rows 0..15: gate features grp*16.., rows 16..31: the matching up rows
-  const int M = a.M;
-  const int t = tid();
-  if (t >= 16 * MAXM) return;
-  const int m = t >> 4, f = t & 15;
-  if (m >= M) return;
-  const float g = rbf(res[f][m]);
-  const float u = rbf(res[16 + f][m]);
-  const float s = rbf(g / (1.0f + expf(-g)));
-  const rsrc_t mr = make_rsrc(m_slot(a, layer), (unsigned)((size_t)M * a.I * 2));
-  stc_b16(mr, (unsigned)((size_t)m * a.I + grp * 16 + f) * 2, f2bf(s * u));
-}
 
 __device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
   const bool an = av != av, bn = bv != bv;
@@ -490,225 +362,200 @@ __device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
   return av > bv || (av == bv && ai < bi);
 }
 
-__device__ __forceinline__ void epi_logits(const Args& a, Shared& sh, float (*res)[MAXM + 1], int grp) {
-  // 32 vocab rows grp*32 ..; logits out + the workgroup's running argmax per token
-  const int M = a.M;
-  const int t = tid();
-  const int m = t >> 5, v = t & 31;
-  float val = -INFINITY;
-  int idx = 0x7fffffff;
-  if (m < M) {
-    const bf16 b = f2bf(res[v][m]);
-    const int col = grp * 32 + v;
-    a.logits[(size_t)m * a.V + col] = b;
-    val = bf2f(b);
-    idx = col;
-  }
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(val, o, 64);
-    const int oi = __shfl_xor(idx, o, 64);
-    if (am_better(ov, oi, val, idx)) { val = ov; idx = oi; }
-  }
-  if (m < M && v == 0 && am_better(val, idx, sh.bestv[m], sh.besti[m])) {
-    sh.bestv[m] = val;
-    sh.besti[m] = idx;
-  }
-}
-
-// Run the epilogue of a row group whose fp32 sums are in res.
-template <int EPI>
-__device__ __forceinline__ void run_epilogue(const Args& a, Shared& sh, float (*res)[MAXM + 1],
-                                             int grp, int layer, unsigned hres) {
-  if (EPI == EPI_QKV) epi_qkv(a, res, layer, grp);
-  else if (EPI == EPI_RES) epi_res(a, res, grp, layer, hres);   // layer: output h slot
-  else if (EPI == EPI_SILU) epi_silu(a, res, grp, layer);
-  else epi_logits(a, sh, res, grp);
-}
-
-// Reduce the waves' tiles of one row group and finish it: directly when this workgroup owns the
-// whole group, else through partials, finished by the last contributor to arrive (partials
-// summed in workgroup order, CB contributors' loads in flight at once; an empty contributor
-// adds +0).
-template <int NR, int EPI>
-__device__ __forceinline__ void flush_group(const Args& a, Shared& sh, const Geo& g, int grp, int layer,
-                            f32x4 (&acc)[NR], int p = -1) {
+// Reduce the waves' tiles of chunk ch and run its epilogue. oslot: QKV/SILU the layer, RES the
+// h slot written (its input is slot oslot - 1, preloaded per thread in hin).
+template <int KIND, int EPI>
+__device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& g, int ch,
+                                          f32x4 (&acc)[mat_T(KIND)], int oslot, unsigned hin) {
+  constexpr int T = mat_T(KIND), CAPU = mat_CAPU(KIND);
   const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
-  GemvLds<NR> L(sh);
-  const unsigned hres = EPI == EPI_RES ? epi_res_input(a, grp, layer) : 0u;
+  const int rows = chunk_rows<KIND>(g, ch);
+  const int ua = g.u0 + ch * CAPU;            // first unit of the chunk
 #pragma unroll
-  for (int t = 0; t < NR; ++t) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) L.red[wave][t][lane * 4 + i] = acc[t][i];
+  for (int t = 0; t < T; ++t) {
+    if (16 * t < rows) *(f32x4*)&sh.u.g.red[wave][t][lane * 4] = acc[t];
     acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes done (vmcnt untouched)
-  __builtin_amdgcn_s_barrier();
+  lds_barrier();
   // res[row][m], row = t*16 + (lane/16)*4 + i of the D layout, m = lane % 16
-  for (int e = tid(); e < NR * 256; e += NTHR) {
+  for (int e = tid(); e < T * 256; e += NTHR) {
     const int t = e >> 8, ln = (e >> 2) & 63, i = e & 3;
-    float s = 0.f;
+    if (16 * t < rows) {
+      float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) s += L.red[w][t][ln * 4 + i];
-    L.res[t * 16 + (ln >> 4) * 4 + i][ln & 15] = s;
+      for (int w = 0; w < NWAVE; ++w) s += sh.u.g.red[w][t][e & 255];
+      sh.u.g.res[t * 16 + (ln >> 4) * 4 + i][ln & 15] = s;
+    }
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-  const int first = wg_of_step(g, grp * g.nk);
-  const int last = wg_of_step(g, (grp + 1) * g.nk - 1);
-  bool finish = true;
-  if (first != last) {
-    // partial: slot 0 = the group holding this workgroup's first step, slot 1 = its last
-    const int rows = NR * 16;
-    const unsigned slot_floats = (unsigned)(rows * MAXM);
-    const rsrc_t pr = make_rsrc(a.ws + a.off_part, (unsigned)(gridDim.x * 2 * slot_floats * 4));
-    const int myslot = (grp == g.s0 / g.nk) ? 0 : 1;
-    // whole [rows][MAXM] tiles (columns >= M carry finite values nobody reads): no division
-    constexpr int PE = NR * 16 * MAXM;       // floats per partial
-    const unsigned mybase = (blockIdx.x * 2 + myslot) * slot_floats * 4;
-    for (int e = tid(); e < PE; e += NTHR) stc_f32(pr, mybase + e * 4, L.res[e >> 4][e & 15]);
-    // contributors: the workgroups first..last whose step range is not empty
-    int ncontrib = 0;
-    for (int c = first; c <= last; ++c) ncontrib += step0_of(g, c + 1) > step0_of(g, c);
-    STEP_TRACE(p, 4);
-    finish = arrive_last(a.ctr + C_GROUP + grp, ncontrib, &sh.flag);
-    STEP_TRACE(p, 5);
-    if (finish) {
-      constexpr int EPT = (PE + NTHR - 1) / NTHR;
-      constexpr int CB = 8;
-      constexpr unsigned NONE = 0x80000000u;  // past the descriptor's range: reads 0
-      float acc[EPT];
+  lds_barrier();
+  const int t = tid();
+  if (EPI == EPI_QKV) {
+    // raw q|k|v columns ua .. ua + rows for every token (q/k RMSNorm, RoPE and the K/V cache
+    // write happen in the attention phase, which holds whole heads)
+    const int nqkv = (a.NH + 2 * a.NKV) * HD;
+    const rsrc_t qr = make_rsrc(qkv_slot(a, oslot), (unsigned)((size_t)M * nqkv * 2));
+    for (int e = t; e < rows * M; e += NTHR) {
+      const int m = e / rows, j = e - m * rows;
+      stc_b16(qr, (unsigned)((size_t)m * nqkv + ua + j) * 2, f2bf(sh.u.g.res[j][m]));
+    }
+  } else if (EPI == EPI_RES) {
+    // residual columns ua .. ua + rows (<= 16): h[oslot] = bf16(h[oslot-1] + bf16(sum));
+    // ss[oslot][wg][m] = sum over the columns of h^2 (thread t < 256: row t / 16, column t % 16)
+    if (t < 256) {
+      const int m = t >> 4, j = t & 15;
+      float q = 0.f;
+      if (m < M && j < rows) {
+        const float hv = rbf(bf2f((bf16)hin) + rbf(sh.u.g.res[j][m]));
+        const rsrc_t hout = make_rsrc(h_slot(a, oslot), (unsigned)((size_t)M * a.H * 2));
+        stc_b16(hout, (unsigned)((size_t)m * a.H + ua + j) * 2, f2bf(hv));
+        q = hv * hv;
+      }
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) acc[i] = 0.f;
-      for (int c0 = first; c0 <= last; c0 += CB) {
-        // contributor record bases (workgroup-uniform), then every load unconditional
-        unsigned cb[CB];
-        int cs = step0_of(g, c0);
-#pragma unroll
-        for (int j = 0; j < CB; ++j) {
-          const int c = c0 + j;
-          const int cn = step0_of(g, c + 1);
-          const bool ok = c <= last && cn > cs;
-          cb[j] = ok ? (unsigned)((c * 2 + (cs >= grp * g.nk ? 0 : 1)) * slot_floats * 4) : NONE;
-          cs = cn;
+      for (int o = 8; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+      if (j == 0) {
+        const rsrc_t ssr = make_rsrc(ss_slot(a, oslot), (unsigned)(gridDim.x * MAXM * 4));
+        stc_f32(ssr, (unsigned)(blockIdx.x * MAXM + m) * 4, q);
+      }
+    }
+  } else if (EPI == EPI_SILU) {
+    // chunk rows 0 .. nf: gate features ua.., rows nf .. 2 nf: the matching up rows
+    const int nf = rows >> 1;
+    const rsrc_t mr = make_rsrc(m_slot(a, oslot), (unsigned)((size_t)M * a.I * 2));
+    for (int e = t; e < nf * M; e += NTHR) {
+      const int m = e / nf, f = e - m * nf;
+      const float gv = rbf(sh.u.g.res[f][m]);
+      const float uv = rbf(sh.u.g.res[nf + f][m]);
+      const float s = rbf(gv / (1.0f + expf(-gv)));
+      stc_b16(mr, (unsigned)((size_t)m * a.I + ua + f) * 2, f2bf(s * uv));
+    }
+  } else {
+    // vocabulary rows ua .. ua + rows: logits out + the workgroup's running argmax per token
+    const int m = t >> 5, v = t & 31;
+    float val = -INFINITY;
+    int idx = 0x7fffffff;
+    if (m < M) {
+      for (int j = v; j < rows; j += 32) {
+        const bf16 bv = f2bf(sh.u.g.res[j][m]);
+        const int col = ua + j;
+        a.logits[(size_t)m * a.V + col] = bv;
+        const float fv = bf2f(bv);
+        if (am_better(fv, col, val, idx)) {
+          val = fv;
+          idx = col;
         }
-        float pv[EPT][CB];
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-          const int e = tid() + i * NTHR;
-#pragma unroll
-          for (int j = 0; j < CB; ++j) pv[i][j] = ldc_f32(pr, (e < PE ? cb[j] : NONE) + e * 4);
-        }
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-#pragma unroll
-          for (int j = 0; j < CB; ++j) acc[i] += pv[i][j];
-      }
-#pragma unroll
-      for (int i = 0; i < EPT; ++i) {
-        const int e = tid() + i * NTHR;
-        if (e < PE) L.res[e >> 4][e & 15] = acc[i];
-      }
-      __syncthreads();
-      STEP_TRACE(p, 6);
-    }
-  }
-  if (finish) run_epilogue<EPI>(a, sh, L.res, grp, layer, hres);
-  if (finish && first != last) STEP_TRACE(p, 7);
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-}
-
-// Consume U wave-steps j0 .. j0+U-1 from a prefetch buffer (static register indices: data still
-// in flight is never copied, so each MFMA waits only for its own loads). A wave's steps inside
-// one batch span at most two row groups (nk >= NWAVE * U): `cur` accumulates the oldest unflushed
-// group, `nxt` the one after it.
-template <int NR>
-__device__ __forceinline__ void gemv_consume(const Geo& g, const u32x4 (&buf)[BATCH], int j0,
-                                             int nmine, int gcur, const unsigned char* xrow_p,
-                                             int ksf, f32x4 (&cur)[NR], f32x4 (&nxt)[NR]) {
-  constexpr int U = BATCH / NR;
-  const int wave = wave_id();
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int j = j0 + u;
-    if (j < nmine) {
-      const int s = g.s0 + wave + NWAVE * j;
-      const int grp = s / g.nk;
-      int w = s - grp * g.nk - ksf;
-      if (w < 0) w += g.nk;
-      const u32x4 xv = *(const u32x4*)(xrow_p + w * 64);
-      if (grp == gcur) {
-#pragma unroll
-        for (int t = 0; t < NR; ++t) cur[t] = mfma16x16x32(buf[u * NR + t], xv, cur[t]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < NR; ++t) nxt[t] = mfma16x16x32(buf[u * NR + t], xv, nxt[t]);
       }
     }
-  }
-}
-
-// Flush the row groups this wave has moved past (all remaining ones when done): every wave of
-// the workgroup flushes every group of the range in order (flush_group synchronises them).
-template <int NR, int EPI>
-__device__ __forceinline__ void gemv_flush_to(const Args& a, Shared& sh, const Geo& g, int layer,
-                                              int target, int seg0, int& flushed,
-                                              f32x4 (&cur)[NR], f32x4 (&nxt)[NR], int p) {
-  while (flushed < target) {
-    flush_group<NR, EPI>(a, sh, g, seg0 + flushed, layer, cur, p);   // leaves cur zeroed
 #pragma unroll
-    for (int t = 0; t < NR; ++t) {
-      cur[t] = nxt[t];
-      nxt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int o = 16; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(val, o, 64);
+      const int oi = __shfl_xor(idx, o, 64);
+      if (am_better(ov, oi, val, idx)) { val = ov; idx = oi; }
     }
-    ++flushed;
+    if (m < M && v == 0 && am_better(val, idx, sh.bestv[m], sh.besti[m])) {
+      sh.bestv[m] = val;
+      sh.besti[m] = idx;
+    }
   }
+  lds_barrier();
 }
 
-// Consume this workgroup's steps of a GEMV phase. On entry A/B hold (in flight) the wave's
-// batches 0 and 1; batches alternate between them. Returns with nothing in flight.
-template <int NR, int EPI>
-__device__ __forceinline__ void gemv_phase(const Args& a, Shared& sh, const Geo& g, int layer,
-                                           u32x4 (&A)[BATCH], u32x4 (&B)[BATCH], int p) {
-  constexpr int U = BATCH / NR;   // steps per batch
-  const int lane = tid() & 63, wave = wave_id();
+// One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, then
+// stream the activation with the remaining weights, one chunk epilogue at a time.
+//   NORM: the input is rmsnorm(x) * lnw, 1/rms from the per-workgroup sums of squares `ss`
+//   EPI_RES: the residual input is h slot oslot - 1, loaded before the wait (it was written two
+//            or more barriers earlier)
+template <int KIND, bool NORM, int EPI>
+__device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool sync, unsigned epoch,
+                                         const bf16* W, int nunits, int K, const bf16* x,
+                                         const bf16* lnw, const float* ss, int oslot) {
+  constexpr int T = mat_T(KIND);
+  constexpr int NSV = MAXG * 4 / NTHR;       // 16-byte sums-of-squares items per thread
+  const Geo g = make_geo<KIND>(W, nunits, K);
   const int M = a.M;
-  const int nmine = g.s1 - g.s0 > wave ? (g.s1 - g.s0 - wave + NWAVE - 1) / NWAVE : 0;
-  const int seg0 = g.s1 > g.s0 ? g.s0 / g.nk : 0;
-  const int nseg = g.s1 > g.s0 ? (g.s1 - 1) / g.nk - seg0 + 1 : 0;
-  const unsigned char* xrow_p =
-      GemvLds<NR>(sh).x + min(lane & 15, M - 1) * sh.xrs + (lane >> 4) * 16;
-  const int ksf = sh.xksf;
-  f32x4 cur[NR], nxt[NR];
+  Buf<KIND> A, B;
+  STEP_TRACE(p, 0);
+  if (sync) bar_arrive(a, epoch);
+  // loads independent of the previous phase, issued first (so they are the first to complete)
+  u32x4 lw = {0u, 0u, 0u, 0u};
+  if (NORM) lw = ldb128(make_rsrc(lnw, (unsigned)(K * 2)), tid() * 8 < K ? (unsigned)(tid() * 16) : OOB);
+  unsigned hin = 0;
+  if (EPI == EPI_RES) {
+    const int m = tid() >> 4, j = tid() & 15;
+    const rsrc_t hr = make_rsrc(h_slot(a, oslot - 1), (unsigned)((size_t)M * a.H * 2));
+    hin = __builtin_amdgcn_raw_buffer_load_b16(
+        hr, tid() < 256 && m < M && j < g.nu ? (unsigned)((size_t)m * a.H + g.u0 + j) * 2 : OOB, 0, 0);
+  }
+  issue_w<KIND>(g, 0, A);
+  issue_w<KIND>(g, 1, B);
+  if (NORM && tid() * 8 < K) *(u32x4*)&sh.lnw[tid() * 8] = lw;
+  if (sync) bar_wait(a, sh, epoch);
+  STEP_TRACE(p, 1);
+  const rsrc_t xr = make_rsrc(x, (unsigned)((size_t)M * K * 2));
+  u32x4 sv[NSV];
+  if (NORM) {
+    // the sums of squares behind 1/rms: [G][16] partials, thread t adds items t, t + NTHR, ..
+    // (16 bytes = 4 rows of one partial; every item of thread t holds rows 4 (t % 4) ..)
+    const rsrc_t ssr = make_rsrc(ss, (unsigned)(gridDim.x * MAXM * 4));
 #pragma unroll
-  for (int t = 0; t < NR; ++t) {
-    cur[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    nxt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  int flushed = 0;
-  // group of the wave's step j
-  auto grp_of = [&](int j) { return (g.s0 + wave + NWAVE * j) / g.nk - seg0; };
-  for (int j0 = 0;; j0 += 2 * U) {
-    if (j0 < nmine) {
-      gemv_consume<NR>(g, A, j0, nmine, seg0 + flushed, xrow_p, ksf, cur, nxt);
-      issue_batch<NR>(g, j0 + 2 * U, A);
-      __builtin_amdgcn_sched_barrier(0);    // keep the refill ahead of the next batch's MFMAs
-      gemv_flush_to<NR, EPI>(a, sh, g, layer, grp_of(min(j0 + U, nmine) - 1), seg0, flushed,
-                             cur, nxt, p);
+    for (int i = 0; i < NSV; ++i) {
+      const int q = tid() + i * NTHR;
+      sv[i] = ldb128(ssr, q < (int)gridDim.x * 4 ? (unsigned)(q * 16) : OOB);
     }
-    if (j0 + U < nmine) {
-      gemv_consume<NR>(g, B, j0 + U, nmine, seg0 + flushed, xrow_p, ksf, cur, nxt);
-      issue_batch<NR>(g, j0 + 3 * U, B);
+  }
+  issue_x<KIND>(g, xr, M, 0, A);
+  issue_x<KIND>(g, xr, M, 1, B);
+  float r = 0.f;
+  if (NORM) {
+    const int lane = tid() & 63, wave = wave_id();
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NSV; ++i)
+      s += f32x4{__uint_as_float(sv[i].x), __uint_as_float(sv[i].y), __uint_as_float(sv[i].z),
+                 __uint_as_float(sv[i].w)};
+#pragma unroll
+    for (int o = 4; o < 64; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] += __shfl_xor(s[i], o, 64);
+    }
+    if (lane < 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sh.rsp[wave][lane * 4 + i] = s[i];
+    }
+    lds_barrier();
+    if (tid() < MAXM) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w) v += sh.rsp[w][tid()];
+      sh.rs[tid()] = rsqrt_ieee(v / (float)a.H + a.eps);
+    }
+    lds_barrier();
+    r = sh.rs[tid() & 15];
+  }
+  STEP_TRACE(p, 2);
+  f32x4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int bi = 0; bi < g.nb; bi += 2) {
+    consume<KIND, NORM>(g, sh, A, bi, r, acc);
+    issue_w<KIND>(g, bi + 2, A);
+    issue_x<KIND>(g, xr, M, bi + 2, A);
+    __builtin_amdgcn_sched_barrier(0);        // keep the refill ahead of the next batch's MFMAs
+    if (bi % g.nbpc == g.nbpc - 1) chunk_end<KIND, EPI>(a, sh, g, bi / g.nbpc, acc, oslot, hin);
+    if (bi + 1 < g.nb) {
+      consume<KIND, NORM>(g, sh, B, bi + 1, r, acc);
+      issue_w<KIND>(g, bi + 3, B);
+      issue_x<KIND>(g, xr, M, bi + 3, B);
       __builtin_amdgcn_sched_barrier(0);
+      if ((bi + 1) % g.nbpc == g.nbpc - 1)
+        chunk_end<KIND, EPI>(a, sh, g, (bi + 1) / g.nbpc, acc, oslot, hin);
     }
-    const bool done = j0 + 2 * U >= nmine;
-    gemv_flush_to<NR, EPI>(a, sh, g, layer,
-                           done ? nseg : grp_of(min(j0 + 2 * U, nmine) - 1), seg0, flushed,
-                           cur, nxt, p);
-    if (done) break;
   }
+  if (EPI == EPI_RES && g.nch == 0 && tid() < MAXM) {   // no columns here: a zero partial
+    const rsrc_t ssr = make_rsrc(ss_slot(a, oslot), (unsigned)(gridDim.x * MAXM * 4));
+    stc_f32(ssr, (unsigned)(blockIdx.x * MAXM + tid()) * 4, 0.f);
+  }
+  STEP_TRACE(p, 3);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -756,12 +603,11 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 // (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
 // many short segments gets fewer blocks.
 constexpr int ATT_OVH = 12;
-constexpr int ATT_REC = HD + 4;      // split partial record: o[128], m, l, 2 pad (16-byte rows)
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
-constexpr int SA_PQ = 3;             // contributors per (row, kv head) whose records the O
-                                     // staging loads in its first pass
+constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
-// units[b]: first partition unit of row b (rows with no keys have none); units[M] = total
+// units[b]: first partition unit of row b (rows with no keys have none); units[M] = total.
+// The partition depends only on this step's positions: computed once per launch.
 __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool flag_errors) {
   if (tid() < 64) {                          // wave 0: lane b = row b, prefix sum by shuffles
     const int b = tid();
@@ -790,38 +636,41 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
   __syncthreads();
 }
 
-// The attention partition depends only on this step's positions: computed once per launch,
-// with the O staging's per-(row, kv head) contributor table (fw, lw, record offsets of the
-// first contributors, S).
-__device__ __forceinline__ void attn_setup(const Args& a, Shared& sh, bool flag_errors) {
-  const int M = a.M, NKV = a.NKV, G = a.NH / a.NKV;
-  attn_partition(a, sh, flag_errors);
-  const int T = sh.units[M];
-  for (int pi = tid(); pi < M * NKV; pi += NTHR) {
-    const int m = pi / NKV, kvh = pi - m * NKV;
-    const int64_t pp = sh.posv[m];
-    const int Lb = (int)min<int64_t>(max<int64_t>(pp + 1, 0), (int64_t)a.cap);
-    const int nblk = (Lb + 31) >> 5;
-    int* pin = sh.pinfo[pi];
-    if (nblk == 0) {
-      pin[0] = 0;
-      pin[1] = -1;                                                  // no keys: zeros
-      for (int q = 0; q < SA_PQ; ++q) pin[2 + q] = -1;
-      continue;
-    }
-    const int S = sh.units[m] + kvh * (ATT_OVH + nblk);
-    const int fw = attn_owner(T, sh.aG, S + ATT_OVH), lw = attn_owner(T, sh.aG, S + ATT_OVH + nblk - 1);
-    pin[0] = fw;
-    pin[1] = lw;
+// Combine the (o, m, l) partials of a (row, kv head) split over attention workgroups fw .. lw
+// (in workgroup order) into the bf16 attention output; run by the last contributor to arrive.
+// Pair start S: a contributor's record is its slot 0 when the pair is its first segment.
+__device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, int layer, int b,
+                                             int kvh, int S, int fw, int lw) {
+  const int NH = a.NH, G = a.NH / a.NKV;
+  const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
+  const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)a.M * NH * HD * 2));
+  for (int e = tid(); e < G * HD; e += NTHR) {
+    const int row = e / HD, d = e - row * HD;
+    float Mx = -INFINITY, l = 0.f, o = 0.f;
+    for (int c0 = fw; c0 <= lw; c0 += ATT_CB) {
+      float mv[ATT_CB], lv[ATT_CB], ov[ATT_CB];
 #pragma unroll
-    for (int q = 0; q < SA_PQ; ++q) {
-      const int c = fw + q;
-      const bool ok = lw > fw && c <= lw && sh.afirst[c + 1] > sh.afirst[c];
-      pin[2 + q] = ok ? (int)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G) * ATT_REC * 4) : -1;
+      for (int j = 0; j < ATT_CB; ++j) {
+        const int c = c0 + j;
+        const bool ok = c <= lw && sh.afirst[c + 1] > sh.afirst[c];
+        const unsigned ro =
+            ok ? (unsigned)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G + row) * ATT_REC) * 4 : OOB;
+        mv[j] = ok ? ldc_f32(pr, ro + HD * 4) : -INFINITY;
+        lv[j] = ldc_f32(pr, ok ? ro + (HD + 1) * 4 : OOB);
+        ov[j] = ldc_f32(pr, ok ? ro + d * 4 : OOB);
+      }
+#pragma unroll
+      for (int j = 0; j < ATT_CB; ++j) {
+        if (mv[j] == -INFINITY) continue;
+        const float Mn = fmaxf(Mx, mv[j]);
+        const float fo = exp2f(Mx - Mn), fn = exp2f(mv[j] - Mn);
+        o = o * fo + ov[j] * fn;
+        l = l * fo + lv[j] * fn;
+        Mx = Mn;
+      }
     }
-    pin[6] = S;
+    stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o * (1.0f / l)));
   }
-  __syncthreads();
 }
 
 __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer, int p) {
@@ -837,6 +686,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
   STEP_TRACE(p, 4);
   const int i0 = sh.afirst[blockIdx.x], i1 = sh.afirst[blockIdx.x + 1];
+  const int Tu = sh.units[M], Ga = sh.aG;
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
   const rsrc_t rawr = make_rsrc(qkv_slot(a, layer), (unsigned)((size_t)M * nqkv * 2));
@@ -1052,7 +902,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       }
       __syncthreads();
       // a (row, kv head) whose blocks all lie in this workgroup is finished here; one split over
-      // workgroups leaves (o, m, l) partials, combined by the O projection's staging
+      // workgroups leaves (o, m, l) partials, combined by its last contributor to arrive
       const bool whole = j0 == 0 && nseg == nblk;
       const int myslot = first_seg ? 0 : 1;
       first_seg = false;
@@ -1080,6 +930,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
           }
         }
       }
+      if (!whole) {
+        const int fw = attn_owner(Tu, Ga, S + ATT_OVH);
+        const int lw = attn_owner(Tu, Ga, S + ATT_OVH + nblk - 1);
+        int nc = 0;
+        for (int c = fw; c <= lw; ++c) nc += sh.afirst[c + 1] > sh.afirst[c];
+        if (arrive_last(a.ctr + C_ATT + bk, nc, &sh.flag))
+          attn_combine(a, sh, layer, b, kvh, S, fw, lw);
+      }
       __syncthreads();
     }
     i = inext;
@@ -1088,30 +946,31 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
 }
 
 // ---------------------------------------------------------------------------------------------
-// embedding gather: workgroup q < H/64 copies columns q*64.. of every row, stores ss[q][m]
+// embedding gather: workgroup c copies the same columns of every row that it owns in the O and
+// down phases, and stores their sums of squares ss[0][c][m]
 __device__ __forceinline__ void embed_phase(const Args& a, Shared& sh) {
   const int M = a.M;
-  const int q = blockIdx.x;
-  if (q >= a.H / SSG) return;
   const int t = tid();
-  const int m = t >> 5, c2 = (t & 31) * 2;
+  if (t >= 256) return;
+  const int c0 = part_lo(a.H, gridDim.x, blockIdx.x), nc = part_lo(a.H, gridDim.x, blockIdx.x + 1) - c0;
+  const int m = t >> 4, j = t & 15;
   float s = 0.f;
-  if (m < M) {
+  if (m < M && j < nc) {
     int64_t tk = a.tok[m];
     if (tk < 0 || tk >= a.V) {
-      if (c2 == 0) atomicOr(a.err, E_TOKEN);
+      if (j == 0) atomicOr(a.err, E_TOKEN);
       tk = 0;
     }
-    const unsigned v2 = *(const unsigned*)(a.embed + (size_t)tk * a.H + q * SSG + c2);
+    const bf16 v = a.embed[(size_t)tk * a.H + c0 + j];
     const rsrc_t hr = make_rsrc(h_slot(a, 0), (unsigned)((size_t)M * a.H * 2));
-    stc_u32(hr, (unsigned)((size_t)m * a.H + q * SSG + c2) * 2, v2);
-    s = lo_bf(v2) * lo_bf(v2) + hi_bf(v2) * hi_bf(v2);
+    stc_b16(hr, (unsigned)((size_t)m * a.H + c0 + j) * 2, v);
+    s = bf2f(v) * bf2f(v);
   }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  if (m < M && (t & 31) == 0) {
-    const rsrc_t ssr = make_rsrc(ss_slot(a, 0), (unsigned)(SS_SLOT * 4));
-    stc_f32(ssr, (unsigned)(q * MAXM + m) * 4, s);
+  for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (j == 0) {
+    const rsrc_t ssr = make_rsrc(ss_slot(a, 0), (unsigned)(gridDim.x * MAXM * 4));
+    stc_f32(ssr, (unsigned)(blockIdx.x * MAXM + m) * 4, s);
   }
 }
 
@@ -1124,152 +983,6 @@ __device__ __forceinline__ int phase_kind(const Args& a, int p, int* layer) {
   if (p == 1 + 5 * a.L) { *layer = -1; return P_LM; }
   *layer = (p - 1) / 5;
   return P_QKV + (p - 1) % 5;
-}
-
-__device__ __forceinline__ bool phase_geo(const Args& a, const Shared& sh, int p, Geo* g) {
-  int layer;
-  const int kind = phase_kind(a, p, &layer);
-  const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
-  switch (kind) {
-    case P_QKV: *g = make_geo(uniform_ptr<const bf16>(lp[F_WQKV]), (a.NH + 2 * a.NKV) * HD, a.H, LNR_QKV, true); return true;
-    case P_O:   *g = make_geo(uniform_ptr<const bf16>(lp[F_WO]), a.H, a.NH * HD, LNR_O, false); return true;
-    case P_GU:  *g = make_geo(uniform_ptr<const bf16>(lp[F_WGU]), 2 * a.I, a.H, LNR_GU, false); return true;
-    case P_D:   *g = make_geo(uniform_ptr<const bf16>(lp[F_WD]), a.H, a.I, LNR_D, false); return true;
-    case P_LM:  *g = make_geo(a.lm_t, a.V, a.H, LNR_LM, true); return true;
-    default: return false;
-  }
-}
-
-// Staging of the O projection's input x = the attention output of `layer`. A (row, kv head)
-// split over attention workgroups is combined here from its (o, m, l) partials (log-sum-exp,
-// online in workgroup order) on the way into LDS, and also written to the attention slot.
-// The partials are write-once per layer (plain cached loads); every load of a thread's items
-// is issued before the first combine.
-constexpr int SA_IPT = 3;            // items per thread per batch
-
-__device__ __forceinline__ void stage_attn(const Args& a, Shared& sh, unsigned char* xb, const Geo& g,
-                                           int layer, int p) {
-  const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
-  const int K = NH * HD;
-  const int t = tid();
-  int ksf = 0, nw = 0;
-  if (g.s1 > g.s0) {
-    ksf = g.s0 % g.nk;
-    nw = min(g.s1 - g.s0, g.nk);
-  }
-  const int xrs = nw * 64 + 16;
-  const int items = M * nw * 4;
-  STEP_TRACE(p, 8);
-  const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * K * 2));
-  const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
-  if (t == 0) {
-    sh.xrs = xrs;
-    sh.xksf = ksf;
-    sh.xnw = nw;
-  }
-  const int gsh = __builtin_ctz(G);
-  for (int base = 0; base < items; base += SA_IPT * NTHR) {
-    int lds[SA_IPT], m_[SA_IPT], pi_[SA_IPT], hh_[SA_IPT], d0_[SA_IPT];
-    unsigned eo_[SA_IPT];
-    u32x4 xd[SA_IPT];
-    float mv[SA_IPT][SA_PQ], lv[SA_IPT][SA_PQ];
-    u32x4 oa[SA_IPT][SA_PQ], ob[SA_IPT][SA_PQ];
-    // pass 1: every load
-#pragma unroll
-    for (int b = 0; b < SA_IPT; ++b) {
-      const int it = base + t + b * NTHR;
-      const bool valid = it < items;
-      const unsigned eo = stage_off(valid ? it : 0, nw > 0 ? nw : 1, ksf, g.nk > 0 ? g.nk : 1, K, &lds[b]);
-      const int m = valid ? it / (nw * 4) : 0;
-      const int col = (int)(eo - (unsigned)m * K);
-      const int h = col >> 7, kvh = h >> gsh;
-      hh_[b] = h & (G - 1);
-      d0_[b] = col & (HD - 1);
-      m_[b] = valid ? m : -1;
-      eo_[b] = eo;
-      const int pi = m * NKV + kvh;
-      pi_[b] = pi;
-      const int fw = sh.pinfo[pi][0], lw = sh.pinfo[pi][1];
-      xd[b] = ldb128(orr, valid && fw == lw ? eo * 2 : 0xfffffff0u);
-      const unsigned hoff = (unsigned)(hh_[b] * ATT_REC * 4);
-#pragma unroll
-      for (int q = 0; q < SA_PQ; ++q) {
-        const int r = sh.pinfo[pi][2 + q];
-        const bool ok = valid && r >= 0;
-        const unsigned ro = (unsigned)r + hoff;
-        mv[b][q] = ok ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + HD * 4, 0, 0)) : -INFINITY;
-        lv[b][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ok ? ro + (HD + 1) * 4 : 0xfffffff0u, 0, 0));
-        oa[b][q] = ldb128(pr, ok ? ro + d0_[b] * 4 : 0xfffffff0u);
-        ob[b][q] = ldb128(pr, ok ? ro + (d0_[b] + 4) * 4 : 0xfffffff0u);
-      }
-    }
-    // pass 2: combine (contributors beyond the first SA_PQ are loaded here, rarely)
-#pragma unroll
-    for (int b = 0; b < SA_IPT; ++b) {
-      if (m_[b] < 0) continue;
-      const int pi = pi_[b];
-      const int fw = sh.pinfo[pi][0], lw = sh.pinfo[pi][1];
-      u32x4 x = xd[b];
-      if (lw > fw) {
-        float Mx = -INFINITY, l = 0.f, o[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = 0.f;
-        auto add = [&](float mq, float lq, u32x4 qa, u32x4 qb) {
-          if (mq == -INFINITY) return;
-          const float Mn = fmaxf(Mx, mq);
-          const float fo = exp2f(Mx - Mn), fn = exp2f(mq - Mn);
-          const float ov[8] = {__uint_as_float(qa.x), __uint_as_float(qa.y), __uint_as_float(qa.z),
-                               __uint_as_float(qa.w), __uint_as_float(qb.x), __uint_as_float(qb.y),
-                               __uint_as_float(qb.z), __uint_as_float(qb.w)};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) o[j] = o[j] * fo + ov[j] * fn;
-          l = l * fo + lq * fn;
-          Mx = Mn;
-        };
-#pragma unroll
-        for (int q = 0; q < SA_PQ; ++q) add(mv[b][q], lv[b][q], oa[b][q], ob[b][q]);
-        const int S = sh.pinfo[pi][6];
-        for (int c = fw + SA_PQ; c <= lw; ++c) {
-          if (sh.afirst[c + 1] <= sh.afirst[c]) continue;
-          const unsigned ro = (unsigned)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G + hh_[b]) * ATT_REC) * 4;
-          add(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + HD * 4, 0, 0)),
-              __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ro + (HD + 1) * 4, 0, 0)),
-              ldb128(pr, ro + d0_[b] * 4), ldb128(pr, ro + (d0_[b] + 4) * 4));
-        }
-        const float il = 1.0f / l;
-        x = u32x4{pk_bf16(o[0] * il, o[1] * il), pk_bf16(o[2] * il, o[3] * il),
-                  pk_bf16(o[4] * il, o[5] * il), pk_bf16(o[6] * il, o[7] * il)};
-        // the attention slot copy is written by one workgroup only: the one whose range holds
-        // this k-step of row group 0
-        if (g.s0 + (lds[b] >> 6) < g.nk) stc_b128(orr, eo_[b] * 2, x);
-      }
-      *(u32x4*)(xb + m_[b] * xrs + lds[b]) = x;
-    }
-  }
-  STEP_TRACE(p, 9);
-  __syncthreads();
-}
-
-// One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, stage
-// the activation window, consume. The prefetch registers live only inside this call.
-template <int LNR, int EPI, bool ATTN_X = false>
-__device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, const Geo& g, int p, int layer,
-                                         bool sync, unsigned epoch, int K, const bf16* src,
-                                         const bf16* lnw, const float* ss) {
-  constexpr int NR = 1 << LNR;
-  u32x4 A[BATCH], B[BATCH];
-  STEP_TRACE(p, 0);
-  if (sync) bar_arrive(a, epoch);
-  issue_batch<NR>(g, 0, A);
-  issue_batch<NR>(g, BATCH / NR, B);
-  const u32x4 lwv = (!ATTN_X && lnw != nullptr) ? lnw_prefetch(g, lnw, K) : u32x4{0u, 0u, 0u, 0u};
-  if (sync) bar_wait(a, sh, epoch);
-  STEP_TRACE(p, 1);
-  if (ATTN_X) stage_attn(a, sh, GemvLds<NR>(sh).x, g, layer >> 1, p);   // layer: output h slot 2l+1
-  else stage_x(a, sh, GemvLds<NR>(sh).x, g, K, src, lnw, lwv, ss, p);
-  STEP_TRACE(p, 2);
-  gemv_phase<NR, EPI>(a, sh, g, layer, A, B, p);
-  STEP_TRACE(p, 3);
 }
 
 __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
@@ -1288,36 +1001,38 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
   {
     // attention phases are p = 2 + 5l: position errors are flagged when one of them runs
     const int l0 = a.phase_begin <= 2 ? 0 : (a.phase_begin - 2 + 4) / 5;
-    attn_setup(a, sh, l0 < a.L && 2 + 5 * l0 < a.phase_end);
+    attn_partition(a, sh, l0 < a.L && 2 + 5 * l0 < a.phase_end);
   }
+  const int nqkv = (a.NH + 2 * a.NKV) * HD;
   for (int p = a.phase_begin; p < a.phase_end; ++p) {
     int layer;
     const int kind = phase_kind(a, p, &layer);
     const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
     const bool sync = p > a.phase_begin;
     if (sync) ++epoch;
-    Geo g;
-    phase_geo(a, sh, p, &g);
     switch (kind) {
       case P_QKV:
-        run_gemv<LNR_QKV, EPI_QKV>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer),
-                                   uniform_ptr<const bf16>(lp[F_LN1]), ss_slot(a, 2 * layer));
+        run_gemv<M_QKV, true, EPI_QKV>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WQKV]),
+                                       nqkv, a.H, h_slot(a, 2 * layer),
+                                       uniform_ptr<const bf16>(lp[F_LN1]), ss_slot(a, 2 * layer), layer);
         break;
       case P_O:
-        run_gemv<LNR_O, EPI_RES, true>(a, sh, g, p, 2 * layer + 1, sync, epoch, a.NH * HD,
-                                 attn_slot(a, layer), nullptr, nullptr);
+        run_gemv<M_O, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WO]), a.H,
+                                      a.NH * HD, attn_slot(a, layer), nullptr, nullptr, 2 * layer + 1);
         break;
       case P_GU:
-        run_gemv<LNR_GU, EPI_SILU>(a, sh, g, p, layer, sync, epoch, a.H, h_slot(a, 2 * layer + 1),
-                                   uniform_ptr<const bf16>(lp[F_LN2]), ss_slot(a, 2 * layer + 1));
+        run_gemv<M_GU, true, EPI_SILU>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WGU]), a.I,
+                                       a.H, h_slot(a, 2 * layer + 1),
+                                       uniform_ptr<const bf16>(lp[F_LN2]), ss_slot(a, 2 * layer + 1),
+                                       layer);
         break;
       case P_D:
-        run_gemv<LNR_D, EPI_RES>(a, sh, g, p, 2 * layer + 2, sync, epoch, a.I, m_slot(a, layer),
-                                 nullptr, nullptr);
+        run_gemv<M_D, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WD]), a.H,
+                                      a.I, m_slot(a, layer), nullptr, nullptr, 2 * layer + 2);
         break;
       case P_LM:
-        run_gemv<LNR_LM, EPI_LOGITS>(a, sh, g, p, 0, sync, epoch, a.H, h_slot(a, 2 * a.L), a.fnorm,
-                                     ss_slot(a, 2 * a.L));
+        run_gemv<M_LM, true, EPI_LOGITS>(a, sh, p, sync, epoch, a.lm_t, a.V, a.H, h_slot(a, 2 * a.L),
+                                         a.fnorm, ss_slot(a, 2 * a.L), 0);
         break;
       default:
         STEP_TRACE(p, 0);
@@ -1378,26 +1093,34 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// weight re-layout into MFMA tile order. Block (group gi, k-step ks, tile t) holds rows
-// src_row(gi, t, r), r = 0..15, columns ks*32 .. +32, lane l's 16 bytes = row l%16, k (l/16)*8.
-// gate/up (gu_I > 0, NR = 2): tile 0 = gate rows gi*16.., tile 1 = up rows gu_I + gi*16...
+// Weight re-layout for the step (one thread per 16 source bytes). Matrix `kind` is split into
+// units (rows; gate/up: features, unit u = gate row u and up row gate_up_I + u) over G
+// workgroups exactly as the step's GEMV phases split it; workgroup c's units are stored from
+// unit u0(c) on (so its region starts at byte u0 * UPR * K * 2), in chunks of up to CAPU units;
+// a chunk of `rows` weight rows (gate rows, then up rows) is k-step-major: row j of k-step ks
+// (32 columns, 64 bytes) at chunk byte (ks * rows + j) * 64.
 __global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst, int N, int K,
-                                   int lnr, int gu_I) {
-  const size_t nblocks = (size_t)(N >> 4) * (K >> 5);
-  const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= nblocks) return;
-  const int lane = threadIdx.x & 63;
-  const int nk = K >> 5;
-  const int NR = 1 << lnr;
-  const size_t step = blk >> lnr;
-  const int t = (int)(blk & (NR - 1));
-  const int gi = (int)(step / nk), ks = (int)(step % nk);
-  const int r = lane & 15;
-  int row;
-  if (gu_I > 0) row = (t == 0 ? 0 : gu_I) + gi * 16 + r;
-  else row = ((gi << lnr) + t) * 16 + r;
-  const u32x4 v = *(const u32x4*)(src + (size_t)row * K + ks * 32 + (lane >> 4) * 8);
-  *(u32x4*)(dst + (blk << 9) + lane * 8) = v;
+                                   int kind, int gate_up_I, int G) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const int q8 = K >> 3;
+  if (idx >= (size_t)N * q8) return;
+  const int r = (int)(idx / q8), q = (int)(idx - (size_t)r * q8);
+  const int UPR = kind == M_GU ? 2 : 1;
+  const int CAPU = kind == M_QKV ? mat_CAPU(M_QKV) : kind == M_O ? mat_CAPU(M_O)
+                 : kind == M_GU ? mat_CAPU(M_GU) : kind == M_D ? mat_CAPU(M_D) : mat_CAPU(M_LM);
+  const int half = UPR == 2 && r >= gate_up_I;
+  const int u = half ? r - gate_up_I : r;
+  const int nunits = UPR == 2 ? gate_up_I : N;
+  const int c = (int)(((unsigned)(u + 1) * (unsigned)G - 1) / (unsigned)nunits);
+  const int u0 = part_lo(nunits, G, c), u1 = part_lo(nunits, G, c + 1);
+  const int ch = (u - u0) / CAPU;
+  const int ua = u0 + ch * CAPU;
+  const int nu = min(CAPU, u1 - ua);
+  const int rows = nu * UPR;
+  const int j = (u - ua) + (half ? nu : 0);
+  const int ks = q >> 2, kq = q & 3;
+  const size_t d = (size_t)ua * UPR * K + ((size_t)ks * rows + j) * 32 + kq * 8;
+  *(u32x4*)(dst + d) = *(const u32x4*)(src + (size_t)r * K + q * 8);
 }
 
 }  // namespace st
@@ -1433,14 +1156,13 @@ static int step_grid(int* G_out) {
   return 0;
 }
 
-struct WsLayout { size_t ss, part, att, am, total; };
+struct WsLayout { size_t ss, att, am, total; };
 
 static WsLayout ws_layout(int L, int G, int G_heads) {
   WsLayout w;
-  w.ss = 0;
-  w.part = (size_t)(2 * L + 1) * SS_SLOT;                   // ss: [2L+1][H/64 <= 64][16]
-  w.att = w.part + (size_t)G * 2 * 128 * MAXM;              // GEMV: 2 slots of <= 128 rows x 16
-  w.am = w.att + (size_t)L * G * 2 * G_heads * ATT_REC;    // attention: per layer, 2 slots
+  w.ss = 0;                                                  // [2L+1][G][16]
+  w.att = w.ss + (size_t)(2 * L + 1) * G * MAXM;
+  w.am = w.att + (size_t)L * G * 2 * G_heads * ATT_REC;      // attention: per layer, 2 slots
   w.total = w.am + (size_t)G * MAXM * 2;
   return w;
 }
@@ -1452,11 +1174,6 @@ DD_API int dd_step_grid(void) {
 
 DD_API int dd_step_counters(void) { return C_TOTAL; }
 
-DD_API int dd_step_nr(int matrix) {
-  const int lnr[5] = {LNR_QKV, LNR_O, LNR_GU, LNR_D, LNR_LM};
-  return matrix >= 0 && matrix < 5 ? 1 << lnr[matrix] : 0;
-}
-
 DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV) {
   int G = 0;
   if (L < 1 || NKV < 1 || NH < NKV || step_grid(&G) != 0) return 0;
@@ -1465,44 +1182,42 @@ DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV) {
 
 DD_API size_t dd_tiled_bytes(int N, int K) { return (size_t)N * K * 2; }
 
-DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
+DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gate_up_I,
                           hipStream_t stream) {
-  DD_REQUIRE(src && dst && K % 32 == 0 && (nr == 1 || nr == 2 || nr == 4 || nr == 8));
-  const int lnr = nr == 1 ? 0 : nr == 2 ? 1 : nr == 4 ? 2 : 3;
-  DD_REQUIRE(N % (16 * nr) == 0);
-  DD_REQUIRE(gate_up_I == 0 || (nr == 2 && N == 2 * gate_up_I));
+  DD_REQUIRE(src && dst && matrix >= 0 && matrix < NMAT && N >= 1 && K >= 256 && K % 256 == 0);
+  DD_REQUIRE((matrix == M_GU) == (gate_up_I > 0));
+  DD_REQUIRE(gate_up_I == 0 || N == 2 * gate_up_I);
   DD_REQUIRE(aligned16(src) && aligned16(dst));
-  const size_t nblocks = (size_t)(N / 16) * (K / 32);
-  hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((nblocks + 3) / 4)), dim3(256), 0, stream,
-                     (const bf16*)src, (bf16*)dst, N, K, lnr, gate_up_I);
+  DD_REQUIRE((long long)N * K < (1ll << 40));
+  int G = 0;
+  const int e = step_grid(&G);
+  if (e != 0) return e;
+  DD_REQUIRE((long long)N * G < (1ll << 32));
+  const size_t n16 = (size_t)N * (K / 8);
+  hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, stream,
+                     (const bf16*)src, (bf16*)dst, N, K, matrix, gate_up_I, G);
   return launch_status();
 }
 
-// Model geometry the phases take (Qwen3 family, head_dim 128); G > 0 also checks that every
-// GEMV phase's staged activation window fits the LDS x buffer with that many workgroups.
+// Model geometry the phases take (Qwen3 family, head_dim 128); G > 0 also checks the split of
+// every GEMV over that many workgroups.
 static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int G) {
   if (!(M >= 1 && M <= MAXM && L >= 1 && NKV >= 1 && NH >= NKV && NH % NKV == 0 &&
         NH / NKV <= MAXG_HEADS && ((NH / NKV) & (NH / NKV - 1)) == 0 && L <= MAXL))
     return false;
   if (MAXM * NKV > C_AM - C_ATT) return false;            // one combine counter per (row, kv head)
-  if (!(H % SSG == 0 && H / SSG <= 64 && I % 16 == 0 && V % 32 == 0)) return false;
-  const int K_of[5] = {H, NH * HD, H, I, H};
-  const int rows_of[5] = {(NH + 2 * NKV) * HD, H, 2 * I, H, V};
-  const int lnr_of[5] = {LNR_QKV, LNR_O, LNR_GU, LNR_D, LNR_LM};
-  const bool whole_of[5] = {true, false, false, false, true};   // as in phase_geo
-  for (int q = 0; q < 5; ++q) {
-    const int K = K_of[q], rows = rows_of[q], lnr = lnr_of[q];
-    if (K % 32 != 0 || rows % (16 << lnr) != 0) return false;
-    const int nk = K / 32;
-    if (nk < NWAVE * (BATCH >> lnr)) return false;       // a batch spans at most two row groups
-    if ((rows >> (4 + lnr)) > C_ATT - C_GROUP) return false;
-    if (G > 0) {
-      const long long S = (long long)(rows >> (4 + lnr)) * nk;
-      const long long per = (S + G - 1) / G;
-      const long long nw = whole_of[q] || per > nk ? nk : per;
-      if ((nw * 64 + 16) * M > (long long)x_capacity(1 << lnr)) return false;
-      if (S * (G + 1) >= (1ll << 31)) return false;           // 32-bit partition arithmetic
-    }
+  // every GEMV K is a whole number of 8-wave rounds of 32-column k-steps; the normalised inputs
+  // (K = H) fit the LDS norm-weight window
+  if (!(H % 256 == 0 && (NH * HD) % 256 == 0 && I % 256 == 0 && H <= MAXH && V >= 1 && I >= 1))
+    return false;
+  if (G > 0) {
+    if (H > 16 * G) return false;                          // O / down: one 16-row tile per WG
+    const long long units[5] = {(long long)(NH + 2 * NKV) * HD, H, I, H, V};
+    for (int q = 0; q < 5; ++q)
+      if (units[q] * G >= (1ll << 32)) return false;      // 32-bit partition arithmetic
+    // a workgroup's weight region stays below 2^31 bytes (32-bit buffer offsets)
+    if ((long long)((V + G - 1) / G) * H * 2 >= (1ll << 31)) return false;
+    if ((long long)((I + G - 1) / G) * 2 * H * 2 >= (1ll << 31)) return false;
   }
   return true;
 }
@@ -1530,6 +1245,8 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, G));
   // attention partition units (32-bit arithmetic in the kernel)
   DD_REQUIRE((long long)MAXM * NKV * (ATT_OVH + cap / 32 + 1) * (G + 1) < (1ll << 31));
+  // K/V cache byte ranges (32-bit buffer offsets)
+  DD_REQUIRE((long long)M * NKV * cap * HD * 2 < (1ll << 32));
   const WsLayout w = ws_layout(L, G, NH / NKV);
   Args a;
   a.layers = layer_table;
@@ -1553,10 +1270,8 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   a.phase_begin = phase_begin;
   a.phase_end = phase_end;
   a.off_ss = (unsigned)w.ss;
-  a.off_part = (unsigned)w.part;
   a.off_att = (unsigned)w.att;
   a.off_am = (unsigned)w.am;
-  a.ws_floats = (unsigned)w.total;
   hipLaunchKernelGGL(decode_step_kernel, dim3(G), dim3(NTHR), sizeof(Shared), stream, a);
   return launch_status();
 }

@@ -44,21 +44,21 @@ class FusedStep:
         self.I = e.layers[0].wd.shape[1]
         if not self.L.dd_step_supported(e.L, self.H, e.nh, e.nkv, self.I, self.V, MAXM):
             raise RuntimeError("dd_step_supported: model geometry not taken by the fused step")
-        # tiles per row group of wqkv, wo, wgu, wd, lm_head: the kernel's compile-time layout
-        nr = [self.L.dd_step_nr(i) for i in range(5)]
+        # matrix kinds of dd_tile_weight: 0 wqkv, 1 wo, 2 wgu, 3 wd, 4 lm_head (each laid out
+        # for the workgroup split of its GEMV phase on this device)
         with torch.no_grad():
             for l in e.layers:
-                l.wqkv_t = self._tile(l.wqkv, nr[0])
-                l.wo_t = self._tile(l.wo, nr[1])
-                l.wgu_t = self._tile(l.wgu, nr[2], gate_up_I=self.I)
-                l.wd_t = self._tile(l.wd, nr[3])
-            self.lm_t = self._tile(e.lm_head, nr[4])
+                l.wqkv_t = self._tile(l.wqkv, 0)
+                l.wo_t = self._tile(l.wo, 1)
+                l.wgu_t = self._tile(l.wgu, 2, gate_up_I=self.I)
+                l.wd_t = self._tile(l.wd, 3)
+            self.lm_t = self._tile(e.lm_head, 4)
         torch.cuda.synchronize(e.dev)
 
-    def _tile(self, w, nr, gate_up_I=0):
+    def _tile(self, w, matrix, gate_up_I=0):
         N, K = w.shape
         out = torch.empty(self.L.dd_tiled_bytes(N, K) // 2, dtype=torch.bfloat16, device=w.device)
-        check(self.L.dd_tile_weight(w.data_ptr(), out.data_ptr(), N, K, nr, gate_up_I,
+        check(self.L.dd_tile_weight(w.data_ptr(), out.data_ptr(), N, K, matrix, gate_up_I,
                                     _stream(w.device)), "dd_tile_weight")
         return out
 

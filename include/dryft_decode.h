@@ -129,24 +129,24 @@ size_t dd_argmax_ws_bytes(int M, int V);
  * device to itself); they meet at grid barriers between phases, each wait bounded by a 200 ms
  * timeout that sets err flag 4 instead of hanging.
  *
- * Weights are streamed from a tiled copy made once by dd_tile_weight (the natural row-major
- * matrices stay the interface): block (row group g, k-step s, tile t) = the 16 x 32 bf16
- * MFMA A-operand of rows (g*nr + t)*16 .. +16, columns s*32 .. +32, 1 KB in lane order
- * (lane l: row l%16, columns (l/16)*8 .. +8). gate_up_I > 0 (nr = 2) interleaves gate and up:
- * tile 0 = gate rows g*16.., tile 1 = up rows gate_up_I + g*16... The nr of each matrix is
- * dd_step_nr(matrix). dst holds dd_tiled_bytes(N, K). */
+ * Weights are streamed from a tiled copy made once per matrix by dd_tile_weight (the natural
+ * row-major matrices stay the interface). matrix: 0 wqkv, 1 wo, 2 wgu (gate_up_I = I, N = 2 I),
+ * 3 wd, 4 lm_head. The matrix is split into units (rows; wgu: features, unit u = gate row u and
+ * up row I + u) over the dd_step_grid() workgroups, workgroup c taking units
+ * [floor(n c / G), floor(n (c + 1) / G)); a workgroup's units are stored in order from byte
+ * u0 * rows_per_unit * K * 2 on, in chunks of up to 32 / 16 / 40 / 16 / 128 units (per matrix as
+ * listed); a chunk of R weight rows (wgu: its gate rows, then its up rows) is k-step-major: the
+ * 32 columns s*32 .. +32 of chunk row j at chunk byte (s * R + j) * 64. K must be a multiple of
+ * 256. dst holds dd_tiled_bytes(N, K); the layout depends on the device's workgroup count. */
 int dd_step_grid(void);
 /* 1 when dd_decode_step takes this model geometry for up to M rows on the current device
- * (head_dim 128; per GEMV phase at least 8 wave-batches of 32-column steps per row group:
- * hidden >= 1024, heads * 128 >= 512, intermediate >= 512; vocab % 32 == 0), else 0. */
+ * (head_dim 128; hidden, heads * 128 and intermediate multiples of 256; hidden <= 4096 and
+ * <= 16 * dd_step_grid()), else 0. */
 int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M);
 int dd_step_counters(void);
-/* Tiles per row group (the nr to pass to dd_tile_weight) of each matrix the step streams:
- * 0 wqkv, 1 wo, 2 wgu (with gate_up_I = I), 3 wd, 4 lm_head; 0 for any other index. */
-int dd_step_nr(int matrix);
 size_t dd_step_ws_bytes(int L, int NH, int NKV);
 size_t dd_tiled_bytes(int N, int K);
-int dd_tile_weight(const void* src, void* dst, int N, int K, int nr, int gate_up_I,
+int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gate_up_I,
                    hipStream_t stream);
 
 /* layer_table: [L][16] int64 device pointers per layer: 0 wqkv (tiled), 1 wo (tiled),

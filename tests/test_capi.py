@@ -49,12 +49,16 @@ def test_validation_rejects_without_launch():
                             1, 9, 32, 8, 128, 128, 128, None) == INVALID         # W*G > 32
     assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
                             1, 1, 32, 8, 128, 128, 100, None) == INVALID         # chunk % 32
-    # weight tiling: nr in {1, 2, 4, 8}, N a multiple of 16 * nr, K of 32, gate/up split = N / 2
-    assert L.dd_tile_weight(fake, fake, 64, 64, 3, 0, None) == INVALID
-    assert L.dd_tile_weight(fake, fake, 48, 64, 2, 0, None) == INVALID
-    assert L.dd_tile_weight(fake, fake, 64, 48, 2, 0, None) == INVALID
-    assert L.dd_tile_weight(fake, fake, 64, 64, 4, 32, None) == INVALID
-    assert L.dd_tile_weight(None, fake, 64, 64, 2, 0, None) == INVALID
+    # weight tiling: matrix 0..4, K a multiple of 256, gate_up_I > 0 exactly for matrix 2 with
+    # N = 2 * gate_up_I
+    assert L.dd_tile_weight(fake, fake, 64, 256, 5, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 256, -1, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 384, 0, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 256, 2, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 256, 2, 48, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 64, 256, 1, 32, None) == INVALID
+    assert L.dd_tile_weight(None, fake, 64, 256, 0, 0, None) == INVALID
+    assert L.dd_tile_weight(ctypes.c_void_p(0x1008), fake, 64, 256, 0, 0, None) == INVALID
 
 
 def _step_args(**kw):
@@ -70,7 +74,7 @@ def _step_args(**kw):
 
 @pytest.mark.parametrize("bad", [
     dict(M=17), dict(M=0), dict(NH=30), dict(cap=0), dict(rope_rows=0), dict(H=2500),
-    dict(V=151930), dict(phase_end=3 + 5 * 36), dict(phase_begin=5, phase_end=5),
+    dict(I=9700), dict(H=4352), dict(V=0), dict(phase_end=3 + 5 * 36), dict(phase_begin=5, phase_end=5),
     dict(tok=None), dict(counters=None), dict(NKV=64, NH=64), dict(rope_rows=(1 << 23) + 1),
 ])
 def test_decode_step_validation(bad):
@@ -97,8 +101,7 @@ def test_host_side_sizing():
         assert L.dd_gemv_counters(N) == -(-N // 16) + 1
     assert L.dd_argmax_ws_bytes(16, 151936) == 16 * 38 * 2 * 4
     assert L.dd_tiled_bytes(6144, 2560) == 6144 * 2560 * 2
-    assert L.dd_step_counters() >= 1024 + 8192
-    assert [L.dd_step_nr(i) for i in range(6)] == [2, 4, 2, 4, 2, 0]
+    assert L.dd_step_counters() >= 1024 + 512
     # attention: chunk multiple of 128, workspace covers every split of every row
     for B, cap in ((1, 640), (16, 3072), (16, 8192)):
         c = L.dd_attn_chunk(B, 8, cap)

@@ -1,6 +1,7 @@
 """Parity of the one-launch decode step (dd_decode_step via FusedStep) against the CPU oracle.
 
-* weight tiling: dd_tile_weight's layout, bit-exact against the same permutation in torch;
+* weight tiling: dd_tile_weight's layout, bit-exact against the same split and permutation in
+  torch;
 * one step from an identical KV cache: the oracle's ``forward_rows`` (per-row positions, the
   reference's ragged semantics) and the fused step start from the same cache bits; logits
   within the north-star gate, argmax equal up to near-ties, K/V written exactly at pos[b]
@@ -26,35 +27,45 @@ def bf16_ulp(x):
     return 2.0 ** (math.floor(math.log2(max(abs(x), 2.0 ** -126))) - 7)
 
 
-def tiled_reference(w, nr, gate_up_I=0):
-    """The tile layout in torch: block (g, s, t) = rows (g*nr + t)*16.., cols s*32.., lane l =
-    row l%16, cols (l/16)*8..+8; gate/up: tile 0 = gate rows g*16.., tile 1 = up rows I+g*16.."""
+CHUNK_UNITS = [32, 16, 40, 16, 128]      # per matrix: 0 wqkv, 1 wo, 2 wgu, 3 wd, 4 lm_head
+
+
+def tiled_reference(w, matrix, G, gate_up_I=0):
+    """The step's weight layout in torch: units (rows; gate/up: features = gate row u and up row
+    I + u) split evenly over G workgroups, each workgroup's units in chunks of CHUNK_UNITS[matrix]
+    units; a chunk's weight rows (gate rows then up rows) stored k-step-major: [nk][rows][32]."""
     N, K = w.shape
     nk = K // 32
-    if gate_up_I:
-        I = gate_up_I
-        g = w[:I].reshape(I // 16, 1, 16, nk, 4, 8)
-        u = w[I:].reshape(I // 16, 1, 16, nk, 4, 8)
-        v = torch.cat([g, u], 1)
-    else:
-        v = w.reshape(N // (16 * nr), nr, 16, nk, 4, 8)
-    return v.permute(0, 3, 1, 4, 2, 5).contiguous().reshape(-1)
+    n = gate_up_I if gate_up_I else N
+    cap = CHUNK_UNITS[matrix]
+    parts = []
+    for c in range(G):
+        u0, u1 = n * c // G, n * (c + 1) // G
+        for ua in range(u0, u1, cap):
+            ub = min(u1, ua + cap)
+            rows = (torch.cat([w[ua:ub], w[gate_up_I + ua:gate_up_I + ub]]) if gate_up_I
+                    else w[ua:ub])
+            parts.append(rows.reshape(-1, nk, 32).permute(1, 0, 2).reshape(-1))
+    return torch.cat(parts)
 
 
-@pytest.mark.parametrize("N,K,nr,gu", [(256, 64, 1, 0), (512, 96, 2, 0), (1024, 160, 4, 0),
-                                      (1536, 256, 8, 0), (384, 192, 2, 192), (6144, 2560, 8, 0)])
-def test_tile_weight_layout(cuda, N, K, nr, gu):
-    from dryft_amd.step import FusedStep  # noqa: F401  (package import)
+@pytest.mark.parametrize("N,K,matrix,gu", [(768, 256, 0, 0), (6144, 2560, 0, 0), (2560, 4096, 1, 0),
+                                          (1024, 512, 1, 0), (19456, 2560, 2, 9728),
+                                          (1024, 1024, 2, 512), (2560, 9728, 3, 0),
+                                          (4096, 1024, 4, 0), (151936, 256, 4, 0), (100, 256, 3, 0)])
+def test_tile_weight_layout(cuda, N, K, matrix, gu):
     from dryft_amd import _lib
     L = _lib.lib()
+    G = L.dd_step_grid()
     g = torch.Generator().manual_seed(N + K)
     w = torch.randn(N, K, generator=g).to(torch.bfloat16)
     wd = w.cuda()
     out = torch.empty(N * K, dtype=torch.bfloat16, device="cuda")
-    _lib.check(L.dd_tile_weight(wd.data_ptr(), out.data_ptr(), N, K, nr, gu,
+    _lib.check(L.dd_tile_weight(wd.data_ptr(), out.data_ptr(), N, K, matrix, gu,
                                 torch.cuda.current_stream().cuda_stream), "tile")
     torch.cuda.synchronize()
-    assert torch.equal(out.cpu().view(torch.int16), tiled_reference(w, nr, gu).view(torch.int16))
+    want = tiled_reference(w, matrix, G, gu)
+    assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
 
 
 def _engine(cfg, seed):
