@@ -54,11 +54,22 @@ constexpr int C_TOTAL = C_AM + 64;
 constexpr int E_TOKEN = 1, E_POS = 2, E_TIMEOUT = 4, E_GEOM = 8;
 
 // The GEMV matrices and their per-workgroup layout: T tiles (16 rows each) per chunk, KB k-steps
-// per prefetch batch, UPR weight rows per unit of the partition (gate/up: one unit = one feature
-// = its gate row and its up row, kept in the same chunk for the SiLU epilogue).
+// per prefetch batch, NBUF batches in the wave's ring (all but the one being consumed are in
+// flight), UPR weight rows per unit of the partition (gate/up: one unit = one feature = its gate
+// row and its up row, kept in the same chunk for the SiLU epilogue).
 enum : int { M_QKV = 0, M_O = 1, M_GU = 2, M_D = 3, M_LM = 4, NMAT = 5 };
+#ifndef DD_KB_OD
+#define DD_KB_OD 8
+#endif
+#ifndef DD_NBUF
+#define DD_NBUF 2
+#endif
+#ifndef DD_NBUF_LM
+#define DD_NBUF_LM 2
+#endif
 __host__ __device__ constexpr int mat_T(int k) { return k == M_QKV ? 2 : k == M_GU ? 5 : k == M_LM ? 8 : 1; }
-__host__ __device__ constexpr int mat_KB(int k) { return k == M_QKV ? 4 : k == M_GU ? 2 : k == M_LM ? 1 : 8; }
+__host__ __device__ constexpr int mat_KB(int k) { return k == M_QKV ? 2 : k == M_GU ? 1 : k == M_LM ? 1 : DD_KB_OD; }
+__host__ __device__ constexpr int mat_NBUF(int k) { return k == M_LM ? DD_NBUF_LM : DD_NBUF; }
 __host__ __device__ constexpr int mat_UPR(int k) { return k == M_GU ? 2 : 1; }
 __host__ __device__ constexpr int mat_CAPU(int k) { return mat_T(k) * 16 / mat_UPR(k); }
 constexpr int TMAX = 8;
@@ -126,6 +137,7 @@ struct Args {
   int L, M, H, NH, NKV, I, V, cap, rope_rows;
   float eps;
   int phase_begin, phase_end;
+  int phase_cur;                     // trace builds: the phase being run
   unsigned off_ss, off_att, off_am;  // workspace offsets (floats); ss: [2L+1][G][16]
 };
 
@@ -372,6 +384,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
   const int M = a.M;
   const int rows = chunk_rows<KIND>(g, ch);
   const int ua = g.u0 + ch * CAPU;            // first unit of the chunk
+  STEP_TRACE(a.phase_cur, 7);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     if (16 * t < rows) *(f32x4*)&sh.u.g.red[wave][t][lane * 4] = acc[t];
@@ -458,6 +471,22 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
     }
   }
   lds_barrier();
+  STEP_TRACE(a.phase_cur, 8);
+}
+
+// Consume batch bi from ring slot b, refill the slot with batch bi + NBUF, finish the chunk when
+// bi is its last batch.
+template <int KIND, bool NORM, int EPI>
+__device__ __forceinline__ void gemv_step(const Args& a, Shared& sh, const Geo& g, rsrc_t xr, Buf<KIND>& b,
+                                          int bi, float r, f32x4 (&acc)[mat_T(KIND)], int oslot,
+                                          unsigned hin) {
+  constexpr int NBUF = mat_NBUF(KIND);
+  if (bi >= g.nb) return;
+  consume<KIND, NORM>(g, sh, b, bi, r, acc);
+  issue_w<KIND>(g, bi + NBUF, b);
+  issue_x<KIND>(g, xr, a.M, bi + NBUF, b);
+  __builtin_amdgcn_sched_barrier(0);          // keep the refill ahead of the next batch's MFMAs
+  if (bi % g.nbpc == g.nbpc - 1) chunk_end<KIND, EPI>(a, sh, g, bi / g.nbpc, acc, oslot, hin);
 }
 
 // One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, then
@@ -469,13 +498,14 @@ template <int KIND, bool NORM, int EPI>
 __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool sync, unsigned epoch,
                                          const bf16* W, int nunits, int K, const bf16* x,
                                          const bf16* lnw, const float* ss, int oslot) {
-  constexpr int T = mat_T(KIND);
+  constexpr int T = mat_T(KIND), NBUF = mat_NBUF(KIND);
   constexpr int NSV = MAXG * 4 / NTHR;       // 16-byte sums-of-squares items per thread
   const Geo g = make_geo<KIND>(W, nunits, K);
   const int M = a.M;
-  Buf<KIND> A, B;
+  Buf<KIND> ring[NBUF];
   STEP_TRACE(p, 0);
   if (sync) bar_arrive(a, epoch);
+  STEP_TRACE(p, 9);
   // loads independent of the previous phase, issued first (so they are the first to complete)
   u32x4 lw = {0u, 0u, 0u, 0u};
   if (NORM) lw = ldb128(make_rsrc(lnw, (unsigned)(K * 2)), tid() * 8 < K ? (unsigned)(tid() * 16) : OOB);
@@ -486,8 +516,8 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
     hin = __builtin_amdgcn_raw_buffer_load_b16(
         hr, tid() < 256 && m < M && j < g.nu ? (unsigned)((size_t)m * a.H + g.u0 + j) * 2 : OOB, 0, 0);
   }
-  issue_w<KIND>(g, 0, A);
-  issue_w<KIND>(g, 1, B);
+#pragma unroll
+  for (int s = 0; s < NBUF; ++s) issue_w<KIND>(g, s, ring[s]);
   if (NORM && tid() * 8 < K) *(u32x4*)&sh.lnw[tid() * 8] = lw;
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
@@ -503,8 +533,8 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
       sv[i] = ldb128(ssr, q < (int)gridDim.x * 4 ? (unsigned)(q * 16) : OOB);
     }
   }
-  issue_x<KIND>(g, xr, M, 0, A);
-  issue_x<KIND>(g, xr, M, 1, B);
+#pragma unroll
+  for (int s = 0; s < NBUF; ++s) issue_x<KIND>(g, xr, M, s, ring[s]);
   float r = 0.f;
   if (NORM) {
     const int lane = tid() & 63, wave = wave_id();
@@ -536,20 +566,9 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
   f32x4 acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int bi = 0; bi < g.nb; bi += 2) {
-    consume<KIND, NORM>(g, sh, A, bi, r, acc);
-    issue_w<KIND>(g, bi + 2, A);
-    issue_x<KIND>(g, xr, M, bi + 2, A);
-    __builtin_amdgcn_sched_barrier(0);        // keep the refill ahead of the next batch's MFMAs
-    if (bi % g.nbpc == g.nbpc - 1) chunk_end<KIND, EPI>(a, sh, g, bi / g.nbpc, acc, oslot, hin);
-    if (bi + 1 < g.nb) {
-      consume<KIND, NORM>(g, sh, B, bi + 1, r, acc);
-      issue_w<KIND>(g, bi + 3, B);
-      issue_x<KIND>(g, xr, M, bi + 3, B);
-      __builtin_amdgcn_sched_barrier(0);
-      if ((bi + 1) % g.nbpc == g.nbpc - 1)
-        chunk_end<KIND, EPI>(a, sh, g, (bi + 1) / g.nbpc, acc, oslot, hin);
-    }
+  for (int bi = 0; bi < g.nb; bi += NBUF) {
+#pragma unroll
+    for (int s = 0; s < NBUF; ++s) gemv_step<KIND, NORM, EPI>(a, sh, g, xr, ring[s], bi + s, r, acc, oslot, hin);
   }
   if (EPI == EPI_RES && g.nch == 0 && tid() < MAXM) {   // no columns here: a zero partial
     const rsrc_t ssr = make_rsrc(ss_slot(a, oslot), (unsigned)(gridDim.x * MAXM * 4));
@@ -673,7 +692,11 @@ __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, in
   }
 }
 
-__device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer, int p) {
+// The attention phase. The K/V cache below each row's position does not depend on this step, so
+// the first round's segments are laid out and every wave's first K/V block is requested before
+// the barrier wait (sync: the phase waits for the QKV phase here).
+__device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int layer, int p, bool sync,
+                                                unsigned epoch) {
   const int M = a.M, NKV = a.NKV, NH = a.NH, G = NH / NKV;
   const int lane = tid() & 63, wave = wave_id();
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -698,8 +721,29 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
   const int maxseg = ATT_QN / G;
   bool first_seg = true;
-  for (int i = i0; i < i1;) {
-    // ---- this round's segments: (row, kv head) pairs whose blocks meet [i, i1)
+  // one 32-key block of K (S^T operand: lane = key l16 of half t, dims kb*32 + g4*8) and V
+  // (rows of 16 keys x 8 dims, transposed through LDS below)
+  u32x4 kreg[2][4], vreg[8];
+  auto load_block = [&](size_t kvbase, int key0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      int key = key0 + t * 16 + l16;
+      key = key < a.cap ? key : a.cap - 1;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int cc = it * 64 + lane;
+      int key = key0 + (cc >> 4);
+      key = key < a.cap ? key : a.cap - 1;
+      vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
+    }
+  };
+  // ---- a round's segments: (row, kv head) pairs whose blocks meet [i, i1), then the wave's
+  // first block of the round's first segment (its latency overlaps the prologue), unless it is
+  // the pair's newest block (whose key at pos the prologue writes)
+  auto start_round = [&](int i) {
     if (tid() == 0) {
       int n = 0, u = i;
       while (u < i1 && n < maxseg) {
@@ -724,37 +768,22 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       sh.segnext = u;                                               // where the next round starts
     }
     __syncthreads();
-    const int nsg = sh.nseg;
-    const int inext = sh.segnext;
-    // one 32-key block of K (S^T operand: lane = key l16 of half t, dims kb*32 + g4*8) and V
-    // (rows of 16 keys x 8 dims, transposed through LDS below)
-    u32x4 kreg[2][4], vreg[8];
-    auto load_block = [&](size_t kvbase, int key0) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        int key = key0 + t * 16 + l16;
-        key = key < a.cap ? key : a.cap - 1;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
-      }
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int cc = it * 64 + lane;
-        int key = key0 + (cc >> 4);
-        key = key < a.cap ? key : a.cap - 1;
-        vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
-      }
-    };
-    // the wave's first block of the round's first segment is loaded before the prologue, so its
-    // latency overlaps the prologue, unless it is the pair's newest block (whose key at pos the
-    // prologue writes)
-    bool pre = false;                        // kreg/vreg hold the wave's next block
-    if (nsg > 0) {
+    bool pre = false;
+    if (sh.nseg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
       const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
       pre = wave < ns && j0 + wave != ((Lb + 31) >> 5) - 1;
       if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
     }
+    return pre;
+  };
+  bool pre = start_round(i0);                // kreg/vreg hold the wave's next block
+  if (sync) bar_wait(a, sh, epoch);
+  STEP_TRACE(p, 1);
+  for (int i = i0; i < i1;) {
+    if (i != i0) pre = start_round(i);
+    const int nsg = sh.nseg;
+    const int inext = sh.segnext;
     // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; the
     // segment holding the newest block also writes K/V of position pos
     for (int task = wave; task < nsg * (G + 2); task += NWAVE) {
@@ -985,7 +1014,8 @@ __device__ __forceinline__ int phase_kind(const Args& a, int p, int* layer) {
   return P_QKV + (p - 1) % 5;
 }
 
-__global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
+__global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
+  Args a = a_in;
   extern __shared__ unsigned char smem_raw[];
   Shared& sh = *(Shared*)smem_raw;
   unsigned epoch = 0;
@@ -1010,6 +1040,9 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
     const long long* lp = layer >= 0 ? sh.ltab[layer] : nullptr;
     const bool sync = p > a.phase_begin;
     if (sync) ++epoch;
+#ifdef DD_STEP_TRACE
+    a.phase_cur = p;
+#endif
     switch (kind) {
       case P_QKV:
         run_gemv<M_QKV, true, EPI_QKV>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WQKV]),
@@ -1036,13 +1069,14 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a) {
         break;
       default:
         STEP_TRACE(p, 0);
-        if (sync) {
-          bar_arrive(a, epoch);
-          bar_wait(a, sh, epoch);
+        if (sync) bar_arrive(a, epoch);
+        if (kind == P_EMB) {
+          if (sync) bar_wait(a, sh, epoch);
+          STEP_TRACE(p, 1);
+          embed_phase(a, sh);
+        } else {
+          attention_phase(a, sh, layer, p, sync, epoch);
         }
-        STEP_TRACE(p, 1);
-        if (kind == P_EMB) embed_phase(a, sh);
-        else attention_phase(a, sh, layer, p);
         STEP_TRACE(p, 3);
         break;
     }
