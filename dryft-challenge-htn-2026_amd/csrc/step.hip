@@ -70,7 +70,14 @@ enum : int { M_QKV = 0, M_O = 1, M_GU = 2, M_D = 3, M_LM = 4, NMAT = 5 };
 __host__ __device__ constexpr int mat_T(int k) { return k == M_QKV ? 2 : k == M_GU ? 5 : k == M_LM ? 8 : 1; }
 __host__ __device__ constexpr int mat_KB(int k) { return k == M_QKV ? 2 : k == M_GU ? 1 : k == M_LM ? 1 : DD_KB_OD; }
 __host__ __device__ constexpr int mat_NBUF(int k) { return k == M_LM ? DD_NBUF_LM : DD_NBUF; }
-__host__ __device__ constexpr int mat_UPR(int k) { return k == M_GU ? 2 : 1; }
+#ifndef DD_OD_TILE
+#define DD_OD_TILE 0
+#endif
+// O / down: units of 16 contiguous rows (whole MFMA tiles, on H / 16 workgroups) when
+// DD_OD_TILE, else single rows (H / G rows on every workgroup)
+__host__ __device__ constexpr int mat_UPR(int k) {
+  return k == M_GU ? 2 : (DD_OD_TILE && (k == M_O || k == M_D)) ? 16 : 1;
+}
 __host__ __device__ constexpr int mat_CAPU(int k) { return mat_T(k) * 16 / mat_UPR(k); }
 constexpr int TMAX = 8;
 
@@ -140,6 +147,13 @@ struct Args {
   int phase_cur;                     // trace builds: the phase being run
   unsigned off_ss, off_att, off_am;  // workspace offsets (floats); ss: [2L+1][G][16]
 };
+
+// Activation slots that feed a GEMV (h, attention output, SiLU output; K columns, M rows) are
+// stored k-step-major: element (m, k) at ((k / 32) * M + m) * 32 + k % 32, so the B operand of one
+// 32-column k-step (all M rows) is M * 64 contiguous bytes: one wave load.
+__device__ __forceinline__ unsigned xoff(int m, int k, int M) {
+  return (unsigned)((((k >> 5) * M + m) << 5) + (k & 31));
+}
 
 // Activation buffers are write-once within a launch: the residual stream h has one slot per
 // phase that produces it (embedding -> 0, O of layer l -> 2l+1, down of layer l -> 2l+2), raw
@@ -330,7 +344,7 @@ __device__ __forceinline__ void issue_x(const Geo& g, rsrc_t xr, int M, int bi, 
   for (int kb = 0; kb < KB; ++kb) {
     const int ks = wave + NWAVE * (bb * KB + kb);
     const bool ok = chok && ks < g.nk;
-    b.x[kb] = ldb128(xr, ok ? (unsigned)(((lane & 15) * g.K + ks * 32 + (lane >> 4) * 8) * 2) : OOB);
+    b.x[kb] = ldb128(xr, ok ? (unsigned)(((ks * M + (lane & 15)) * 32 + (lane >> 4) * 8) * 2) : OOB);
   }
 }
 
@@ -384,6 +398,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
   const int M = a.M;
   const int rows = chunk_rows<KIND>(g, ch);
   const int ua = g.u0 + ch * CAPU;            // first unit of the chunk
+  const int r0 = ua * mat_UPR(KIND);          // its first output row (contiguous-unit matrices)
   STEP_TRACE(a.phase_cur, 7);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -410,7 +425,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
     const rsrc_t qr = make_rsrc(qkv_slot(a, oslot), (unsigned)((size_t)M * nqkv * 2));
     for (int e = t; e < rows * M; e += NTHR) {
       const int m = e / rows, j = e - m * rows;
-      stc_b16(qr, (unsigned)((size_t)m * nqkv + ua + j) * 2, f2bf(sh.u.g.res[j][m]));
+      stc_b16(qr, (unsigned)((size_t)m * nqkv + r0 + j) * 2, f2bf(sh.u.g.res[j][m]));
     }
   } else if (EPI == EPI_RES) {
     // residual columns ua .. ua + rows (<= 16): h[oslot] = bf16(h[oslot-1] + bf16(sum));
@@ -421,7 +436,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
       if (m < M && j < rows) {
         const float hv = rbf(bf2f((bf16)hin) + rbf(sh.u.g.res[j][m]));
         const rsrc_t hout = make_rsrc(h_slot(a, oslot), (unsigned)((size_t)M * a.H * 2));
-        stc_b16(hout, (unsigned)((size_t)m * a.H + ua + j) * 2, f2bf(hv));
+        stc_b16(hout, xoff(m, r0 + j, M) * 2, f2bf(hv));
         q = hv * hv;
       }
 #pragma unroll
@@ -440,7 +455,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
       const float gv = rbf(sh.u.g.res[f][m]);
       const float uv = rbf(sh.u.g.res[nf + f][m]);
       const float s = rbf(gv / (1.0f + expf(-gv)));
-      stc_b16(mr, (unsigned)((size_t)m * a.I + ua + f) * 2, f2bf(s * uv));
+      stc_b16(mr, xoff(m, ua + f, M) * 2, f2bf(s * uv));
     }
   } else {
     // vocabulary rows ua .. ua + rows: logits out + the workgroup's running argmax per token
@@ -450,7 +465,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
     if (m < M) {
       for (int j = v; j < rows; j += 32) {
         const bf16 bv = f2bf(sh.u.g.res[j][m]);
-        const int col = ua + j;
+        const int col = r0 + j;
         a.logits[(size_t)m * a.V + col] = bv;
         const float fv = bf2f(bv);
         if (am_better(fv, col, val, idx)) {
@@ -513,8 +528,10 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
   if (EPI == EPI_RES) {
     const int m = tid() >> 4, j = tid() & 15;
     const rsrc_t hr = make_rsrc(h_slot(a, oslot - 1), (unsigned)((size_t)M * a.H * 2));
+    constexpr int UPR = mat_UPR(KIND);
     hin = __builtin_amdgcn_raw_buffer_load_b16(
-        hr, tid() < 256 && m < M && j < g.nu ? (unsigned)((size_t)m * a.H + g.u0 + j) * 2 : OOB, 0, 0);
+        hr, tid() < 256 && m < M && j < g.nu * UPR ? xoff(m, g.u0 * UPR + j, M) * 2 : OOB,
+        0, 0);
   }
 #pragma unroll
   for (int s = 0; s < NBUF; ++s) issue_w<KIND>(g, s, ring[s]);
@@ -688,7 +705,7 @@ __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, in
         Mx = Mn;
       }
     }
-    stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o * (1.0f / l)));
+    stc_b16(orr, xoff(b, (kvh * G + row) * HD + d, a.M) * 2, f2bf(o * (1.0f / l)));
   }
 }
 
@@ -949,7 +966,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
           l += sh.ls[w][row] * f;
         }
         if (whole) {
-          stc_b16(orr, (unsigned)(((size_t)b * NH + kvh * G + row) * HD + d) * 2, f2bf(o / l));
+          stc_b16(orr, xoff(b, (kvh * G + row) * HD + d, M) * 2, f2bf(o / l));
         } else {
           const unsigned pb = (unsigned)(((blockIdx.x * 2 + myslot) * G + row) * rec) * 4;
           stc_f32(pr, pb + d * 4, o);
@@ -992,7 +1009,7 @@ __device__ __forceinline__ void embed_phase(const Args& a, Shared& sh) {
     }
     const bf16 v = a.embed[(size_t)tk * a.H + c0 + j];
     const rsrc_t hr = make_rsrc(h_slot(a, 0), (unsigned)((size_t)M * a.H * 2));
-    stc_b16(hr, (unsigned)((size_t)m * a.H + c0 + j) * 2, v);
+    stc_b16(hr, xoff(m, c0 + j, M) * 2, v);
     s = bf2f(v) * bf2f(v);
   }
 #pragma unroll
@@ -1050,7 +1067,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
                                        uniform_ptr<const bf16>(lp[F_LN1]), ss_slot(a, 2 * layer), layer);
         break;
       case P_O:
-        run_gemv<M_O, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WO]), a.H,
+        run_gemv<M_O, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WO]), a.H / mat_UPR(M_O),
                                       a.NH * HD, attn_slot(a, layer), nullptr, nullptr, 2 * layer + 1);
         break;
       case P_GU:
@@ -1060,7 +1077,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
                                        layer);
         break;
       case P_D:
-        run_gemv<M_D, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WD]), a.H,
+        run_gemv<M_D, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WD]), a.H / mat_UPR(M_D),
                                       a.I, m_slot(a, layer), nullptr, nullptr, 2 * layer + 2);
         break;
       case P_LM:
@@ -1139,19 +1156,20 @@ __global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restric
   const int q8 = K >> 3;
   if (idx >= (size_t)N * q8) return;
   const int r = (int)(idx / q8), q = (int)(idx - (size_t)r * q8);
-  const int UPR = kind == M_GU ? 2 : 1;
+  const int UPR = kind == M_GU ? 2 : kind == M_O ? mat_UPR(M_O) : kind == M_D ? mat_UPR(M_D) : 1;
   const int CAPU = kind == M_QKV ? mat_CAPU(M_QKV) : kind == M_O ? mat_CAPU(M_O)
                  : kind == M_GU ? mat_CAPU(M_GU) : kind == M_D ? mat_CAPU(M_D) : mat_CAPU(M_LM);
-  const int half = UPR == 2 && r >= gate_up_I;
-  const int u = half ? r - gate_up_I : r;
-  const int nunits = UPR == 2 ? gate_up_I : N;
+  const bool gu = kind == M_GU;
+  const int half = gu && r >= gate_up_I;
+  const int u = gu ? (half ? r - gate_up_I : r) : r / UPR;   // unit of row r
+  const int nunits = gu ? gate_up_I : N / UPR;
   const int c = (int)(((unsigned)(u + 1) * (unsigned)G - 1) / (unsigned)nunits);
   const int u0 = part_lo(nunits, G, c), u1 = part_lo(nunits, G, c + 1);
   const int ch = (u - u0) / CAPU;
   const int ua = u0 + ch * CAPU;
   const int nu = min(CAPU, u1 - ua);
   const int rows = nu * UPR;
-  const int j = (u - ua) + (half ? nu : 0);
+  const int j = gu ? (u - ua) + (half ? nu : 0) : r - ua * UPR;
   const int ks = q >> 2, kq = q & 3;
   const size_t d = (size_t)ua * UPR * K + ((size_t)ks * rows + j) * 32 + kq * 8;
   *(u32x4*)(dst + d) = *(const u32x4*)(src + (size_t)r * K + q * 8);

@@ -75,7 +75,7 @@ class FusedStep:
         f = _State()
         L = e.L
         # write-once activation slots (see dd_decode_step): h per producing phase, the others
-        # per layer
+        # per layer; h, attn and mbuf slots are k-step-major ([K/32][B][32]), qkv row-major
         f.h = torch.empty(2 * L + 1, B, H, **bf)
         f.qkv = torch.empty(L, B, (e.nh + 2 * e.nkv) * HD, **bf)
         f.attn = torch.empty(L, B, e.nh * HD, **bf)

@@ -154,10 +154,11 @@ int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gat
  * 7 k_norm, 8 K cache, 9 V cache ([M, NKV, cap, 128] each); 10..15 unused.
  * tok/pos: [M] int64 (in: this step's tokens and positions; out: the argmax tokens, pos + 1).
  * Activation buffers (bf16), written once per launch (one slot per producing phase, so they
- * are read with plain cached loads): h [2L+1, M, H] (slot 0 embedding, 2l+1 after layer l's
- * O projection, 2l+2 after its down projection), qkv [L, M, (NH + 2 NKV) * 128] (raw q|k|v
- * projection), attn [L, M, NH*128], mbuf [L, M, I]; logits [M, V] hold the step's lm_head
- * output afterwards. ws: dd_step_ws_bytes; counters: dd_step_counters() zeroed ints.
+ * are read with plain cached loads): h [2L+1] slots of M x H (slot 0 embedding, 2l+1 after layer
+ * l's O projection, 2l+2 after its down projection), qkv [L, M, (NH + 2 NKV) * 128] (raw q|k|v
+ * projection, row-major), attn [L] slots of M x NH*128, mbuf [L] slots of M x I; the h, attn and
+ * mbuf slots are k-step-major: element (m, k) of a slot at ((k / 32) * M + m) * 32 + k % 32.
+ * logits [M, V] (row-major) hold the step's lm_head output afterwards. ws: dd_step_ws_bytes; counters: dd_step_counters() zeroed ints.
  * phase_begin/phase_end select a sub-range of the 2 + 5L phases (0 embedding, 1 + 5l + {0 QKV,
  * 1 attention, 2 O, 3 gate/up, 4 down}, 1 + 5L lm_head/argmax); a full step is 0 .. 2 + 5L. */
 int dd_decode_step(const int64_t* layer_table, int L, const void* embed, const void* lm_tiled,

@@ -224,11 +224,13 @@ def test_fused_phases_per_kernel(cuda, shape):
     pos = st.pos.cpu().clone()
     kc0, vc0 = st.kc[0].cpu(), st.vc[0].cpu()
     cpu = lambda t: t.cpu()
+    # h, attention and SiLU slots are k-step-major ([K/32][M][32]); raw q|k|v is row-major
+    rows = lambda t: t.cpu().reshape(-1, B, 32).permute(1, 0, 2).reshape(B, -1)
 
     # the step's activation buffers are write-once slots: h[0] embedding, h[1] after O, h[2]
     # after down; raw q|k|v, attention output and SiLU output one slot per layer
     eng.step.run(st, 0, 2)                                   # embedding + QKV projection
-    h = cpu(f.h[0])
+    h = rows(f.h[0])
     assert torch.equal(h.view(torch.int16), ref.embed[tok].view(torch.int16))
     qkv = ops.linear(ops.rms(h, rl.ln1), rl.wqkv)
     _close(cpu(f.qkv[0]), qkv, "qkv projection")
@@ -251,19 +253,19 @@ def test_fused_phases_per_kernel(cuda, shape):
     # O + residual; a (row, kv head) split over attention workgroups is combined from its
     # partials while O stages its input (and written to the attention slot there)
     eng.step.run(st, 3, 4)
-    attn = cpu(f.attn[0])
+    attn = rows(f.attn[0])
     _close(attn, o, "attention")
-    h1 = cpu(f.h[1])
+    h1 = rows(f.h[1])
     want_h1, _ = ops.linear_add_norm(attn, rl.wo, h, rl.ln2)
     _close(h1, want_h1, "O + residual")
 
     eng.step.run(st, 4, 5)                                   # gate/up + SiLU (RMSNorm on the way in)
     m = ops.gate_up_silu(ops.rms(h1, rl.ln2), rl.wgu)
-    _close(cpu(f.mbuf[0]), m, "gate/up + SiLU")
+    _close(rows(f.mbuf[0]), m, "gate/up + SiLU")
 
-    mb = cpu(f.mbuf[0])
+    mb = rows(f.mbuf[0])
     eng.step.run(st, 5, 6)                                   # down + residual
-    h2 = cpu(f.h[2])
+    h2 = rows(f.h[2])
     want_h2, _ = ops.linear_add_norm(mb, rl.wd, h1, ref.norm)
     _close(h2, want_h2, "down + residual")
 
