@@ -1226,6 +1226,28 @@ DD_API int dd_step_grid(void) {
 
 DD_API int dd_step_counters(void) { return C_TOTAL; }
 
+// Zeroed counters for dd_decode_step in uncached device memory: the barrier and hand-off atomics
+// and polls are served by memory directly instead of passing through the per-XCD L2s (faster
+// under the decode step's streaming load). The memory is never freed: uncached memory must stay
+// mapped for the life of the process once a kernel has read it.
+DD_API int dd_step_counters_alloc(void** out) {
+  DD_REQUIRE(out != nullptr);
+  void* p = nullptr;
+  hipError_t e = hipExtMallocWithFlags(&p, C_TOTAL * sizeof(int), hipDeviceMallocUncached);
+  if (e != hipSuccess) return (int)e;
+  e = hipMemset(p, 0, C_TOTAL * sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return (int)e;
+  *out = p;
+  return 0;
+}
+
+// Diagnostics: copy the dd_step_counters() ints at `counters` to host memory (synchronous).
+DD_API int dd_step_counters_read(const void* counters, int* host) {
+  DD_REQUIRE(counters != nullptr && host != nullptr);
+  return (int)hipMemcpy(host, counters, C_TOTAL * sizeof(int), hipMemcpyDeviceToHost);
+}
+
 DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV) {
   int G = 0;
   if (L < 1 || NKV < 1 || NH < NKV || step_grid(&G) != 0) return 0;

@@ -14,6 +14,7 @@ Same arithmetic and rounding points as ``HipOps`` / the reference ``_TorchOps``;
 the per-op ``HipOps`` graph otherwise (both are HIP; there is no CPU path).
 """
 import ctypes
+import os
 
 import torch
 
@@ -85,7 +86,15 @@ class FusedStep:
         if ws == 0:
             raise RuntimeError("dd_step_ws_bytes rejected the shape")
         f.ws = torch.empty(ws // 4, dtype=torch.float32, device=dev)
-        f.counters = torch.zeros(self.L.dd_step_counters(), dtype=torch.int32, device=dev)
+        # counters in uncached device memory (never freed; the library allocates them), unless
+        # DD_UC_COUNTERS=0 asks for an ordinary zeroed tensor
+        if os.environ.get("DD_UC_COUNTERS", "1") != "0":
+            ptr = ctypes.c_void_p()
+            check(self.L.dd_step_counters_alloc(ctypes.byref(ptr)), "dd_step_counters_alloc")
+            f.counters_ptr = ptr.value
+        else:
+            f.counters = torch.zeros(self.L.dd_step_counters(), dtype=torch.int32, device=dev)
+            f.counters_ptr = f.counters.data_ptr()
         f.err = torch.zeros(1, dtype=torch.int32, device=dev)
         table = torch.zeros(e.L, NFIELD, dtype=torch.int64)
         for i, l in enumerate(e.layers):
@@ -106,11 +115,19 @@ class FusedStep:
             f.table.data_ptr(), e.L, e.embed.data_ptr(), self.lm_t.data_ptr(), e.norm.data_ptr(),
             e.cos.data_ptr(), e.sin.data_ptr(), e.cos.shape[0], st.tok.data_ptr(),
             st.pos.data_ptr(), f.h.data_ptr(), f.qkv.data_ptr(), f.attn.data_ptr(),
-            f.mbuf.data_ptr(), f.logits.data_ptr(), f.ws.data_ptr(), f.counters.data_ptr(),
+            f.mbuf.data_ptr(), f.logits.data_ptr(), f.ws.data_ptr(), f.counters_ptr,
             f.err.data_ptr(), st.B, self.H, e.nh, e.nkv, self.I, self.V, st.cap,
             ctypes.c_float(e.eps), phase_begin, phase_end, _stream(e.dev)),
             "dd_decode_step")
         return f.logits
+
+
+    def counters(self, st):
+        """Host copy of a state's step counters (diagnostics: zero between steps)."""
+        n = self.L.dd_step_counters()
+        host = (ctypes.c_int * n)()
+        check(self.L.dd_step_counters_read(st.fused.counters_ptr, host), "dd_step_counters_read")
+        return list(host)
 
 
 class _State:

@@ -144,6 +144,14 @@ int dd_step_grid(void);
  * <= 16 * dd_step_grid()), else 0. */
 int dd_step_supported(int L, int H, int NH, int NKV, int I, int V, int M);
 int dd_step_counters(void);
+/* Allocates dd_step_counters() zeroed ints for dd_decode_step in uncached device memory (the
+ * barrier and hand-off atomics and polls are then served by memory directly, not through the
+ * per-XCD L2s) and stores the device pointer in *out. The memory is never freed (uncached memory
+ * must stay mapped for the life of the process once a kernel has read it). No counterpart in the
+ * reference: the caller-owned counters of the persistent step. */
+int dd_step_counters_alloc(void** out);
+/* Diagnostics: synchronous copy of the dd_step_counters() ints at `counters` to `host`. */
+int dd_step_counters_read(const void* counters, int* host);
 size_t dd_step_ws_bytes(int L, int NH, int NKV);
 size_t dd_tiled_bytes(int N, int K);
 int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gate_up_I,

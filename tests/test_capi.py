@@ -58,6 +58,10 @@ def test_validation_rejects_without_launch():
     assert L.dd_tile_weight(fake, fake, 64, 256, 2, 48, None) == INVALID
     assert L.dd_tile_weight(fake, fake, 64, 256, 1, 32, None) == INVALID
     assert L.dd_tile_weight(None, fake, 64, 256, 0, 0, None) == INVALID
+    # uncached step counters: an output pointer is required; read-back needs both pointers
+    assert L.dd_step_counters_alloc(None) == INVALID
+    assert L.dd_step_counters_read(None, fake) == INVALID
+    assert L.dd_step_counters_read(fake, None) == INVALID
     assert L.dd_tile_weight(ctypes.c_void_p(0x1008), fake, 64, 256, 0, 0, None) == INVALID
 
 
