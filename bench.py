@@ -155,6 +155,44 @@ def run_decode(torch, eng, prompts, warmup, steps):
     return ms, bytes_step, float(pos0.float().mean()) + steps / 2
 
 
+def run_verify(torch, eng, prompts, W=5, steps=20):
+    """configs[4]'s verify-shaped step: B rows x W tokens (1 + 4 draft ids) at per-row start
+    positions through Engine.verify_logits (the reference's multi-query forward,
+    engine.py:542-547), captured in a hipGraph and replayed; returns (ms/step, bytes/step)."""
+    B = len(prompts)
+    S = max(len(p) for p in prompts)
+    cap = -(-(S + W + 1) // 128) * 128
+    st = eng._new_state(B, cap, W=W)
+    eng._prefill(prompts, st)
+    g = torch.Generator().manual_seed(1)
+    drafts = torch.randint(0, eng.cfg["vocab_size"], (B, W), generator=g).cuda()
+    spos = torch.tensor([len(p) for p in prompts], dtype=torch.long).cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            eng.verify_logits(st, drafts, spos)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eng.verify_logits(st, drafts, spos)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ctx = sum(len(p) + W for p in prompts)
+    bytes_step = weight_bytes(eng.cfg) + KV_BYTES_TOKEN * ctx + KV_BYTES_TOKEN * B * W
+    del graph, st
+    torch.cuda.empty_cache()
+    return ms, bytes_step
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +202,7 @@ def main():
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -211,6 +250,15 @@ def main():
                        "step_achieved_GBps": round(bytes1 / (ms1 * 1e-3) / 1e9, 1),
                        "frac_of_measured": round(bytes1 / (ms1 * 1e-3) / read_bw, 4)}
         print(f"[bench] B=1: {ms1:.3f} ms/step, {1e3 / ms1:.0f} tok/s", file=sys.stderr, flush=True)
+
+    if not args.no_verify:                    # configs[4] verify shape: W = 5 per row
+        msv, bytesv = run_verify(torch, eng, prompts)
+        extra["verify_w5"] = {"ms_per_step": round(msv, 4), "tokens_per_step": B * 5,
+                              "tok_s": round(B * 5 / (msv * 1e-3), 1),
+                              "step_achieved_GBps": round(bytesv / (msv * 1e-3) / 1e9, 1),
+                              "path": "per-op HIP kernels (q/k norm + RoPE + K/V write, "
+                                      "attention) and hipBLASLt GEMMs at M=80, hipGraph"}
+        print(f"[bench] verify B={B} W=5: {msv:.3f} ms/step", file=sys.stderr, flush=True)
 
     roof = step_roofline(ms, bytes_step, B)
     print(f"[bench] roofline {roof}", file=sys.stderr, flush=True)
