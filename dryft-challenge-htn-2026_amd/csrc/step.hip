@@ -635,10 +635,12 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
   return c >= Ga ? T : (int)((unsigned)T * c / Ga);
 }
 
-// Partition units of one (row, kv head): ATT_OVH units for its fixed per-segment latency
+// Partition units of one (row, kv head): att_ovh(M) units for its fixed per-segment latency
 // (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
-// many short segments gets fewer blocks.
-constexpr int ATT_OVH = 12;
+// many short segments gets fewer blocks. With one or two rows the few pairs are spread over more
+// workgroups by a larger weight (measured: B = 1 2.32 vs 2.38 ms per step, B = 16 best at 12).
+constexpr int ATT_OVH_MAX = 24;
+__host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? ATT_OVH_MAX : 12; }
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
@@ -654,7 +656,7 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
         atomicOr(a.err, E_POS);
       const int Lb = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
       const int nblk = (Lb + 31) >> 5;
-      cnt = nblk > 0 ? a.NKV * (ATT_OVH + nblk) : 0;
+      cnt = nblk > 0 ? a.NKV * (att_ovh(a.M) + nblk) : 0;
     }
     int inc = cnt;
 #pragma unroll
@@ -768,14 +770,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         while (b + 1 < M && sh.units[b + 1] <= u) ++b;
         const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
         const int nblk = (Lb + 31) >> 5;
-        const int per = ATT_OVH + nblk;
+        const int per = att_ovh(M) + nblk;
         const int kvh = (u - sh.units[b]) / per;
         const int S = sh.units[b] + kvh * per;                      // pair start (overhead units)
-        const int lo = max(u, S + ATT_OVH), hi = min(i1, S + per);
+        const int lo = max(u, S + att_ovh(M)), hi = min(i1, S + per);
         if (hi > lo) {
           sh.seg[n][0] = b;
           sh.seg[n][1] = kvh;
-          sh.seg[n][2] = lo - S - ATT_OVH;
+          sh.seg[n][2] = lo - S - att_ovh(M);
           sh.seg[n][3] = hi - lo;
           ++n;
         }
@@ -846,7 +848,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       const int nblk = (Lb + 31) >> 5;
       const int bk = b * NKV + kvh;
       const size_t kvbase = (size_t)bk * a.cap * HD;
-      const int S = sh.units[b] + kvh * (ATT_OVH + nblk);
+      const int S = sh.units[b] + kvh * (att_ovh(M) + nblk);
       // Q^T operand (rows = the G query heads of this kv head; rows >= G zero)
       u32x4 qreg[4];
 #pragma unroll
@@ -977,8 +979,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         }
       }
       if (!whole) {
-        const int fw = attn_owner(Tu, Ga, S + ATT_OVH);
-        const int lw = attn_owner(Tu, Ga, S + ATT_OVH + nblk - 1);
+        const int fw = attn_owner(Tu, Ga, S + att_ovh(M));
+        const int lw = attn_owner(Tu, Ga, S + att_ovh(M) + nblk - 1);
         int nc = 0;
         for (int c = fw; c <= lw; ++c) nc += sh.afirst[c + 1] > sh.afirst[c];
         if (arrive_last(a.ctr + C_ATT + bk, nc, &sh.flag))
@@ -1318,7 +1320,7 @@ DD_API int dd_decode_step(const int64_t* layer_table, int L, const void* embed, 
   if (e != 0) return e;
   DD_REQUIRE(geometry_ok(L, H, NH, NKV, I, V, M, G));
   // attention partition units (32-bit arithmetic in the kernel)
-  DD_REQUIRE((long long)MAXM * NKV * (ATT_OVH + cap / 32 + 1) * (G + 1) < (1ll << 31));
+  DD_REQUIRE((long long)MAXM * NKV * (ATT_OVH_MAX + cap / 32 + 1) * (G + 1) < (1ll << 31));
   // K/V cache byte ranges (32-bit buffer offsets)
   DD_REQUIRE((long long)M * NKV * cap * HD * 2 < (1ll << 32));
   const WsLayout w = ws_layout(L, G, NH / NKV);
