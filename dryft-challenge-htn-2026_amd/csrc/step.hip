@@ -193,6 +193,7 @@ constexpr int MAXG_HEADS = 8;                 // query heads per kv head
 constexpr int MAXL = 64;                      // layers
 constexpr int LFIELDS = 10;                   // layer-table fields the phases read
 constexpr int MAXH = 4096;                    // hidden size (norm weight staged in LDS)
+constexpr int ATT_MAXSEG = 8;                 // attention segments of one round
 
 struct Shared {
   union {
@@ -204,6 +205,7 @@ struct Shared {
       bf16 v[NWAVE][32][HD + 8];
       float mrg[NWAVE][MAXG_HEADS][HD];
       bf16 qn[32][HD];                        // normalised, rotated query heads of the segments
+      bf16 kvn[2 * ATT_MAXSEG][HD];           // per segment: k (normalised, rotated), v of pos
     } a;
   } u;
   bf16 lnw[MAXH];                             // norm weight of a normalised-input GEMV phase
@@ -601,7 +603,8 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
 // segments, one per (row, kv head) it touches; its 8 waves share a segment's blocks.
 // Per segment: the G query heads are RMS-normalised and rotated from the raw q|k|v (engine.py
 // qkv_post), the segment holding the newest block also normalises/rotates k and writes K/V at
-// pos; then S^T = K.Q^T and O^T += V^T.P^T on MFMA (P rounded to bf16), the waves merge through
+// pos (its newest block takes key pos from those values, so nothing waits for the cache write);
+// then S^T = K.Q^T and O^T += V^T.P^T on MFMA (P rounded to bf16), the waves merge through
 // LDS, and a (row, kv head) split over workgroups is combined (log-sum-exp, in workgroup order)
 // by the last contributor to arrive.
 
@@ -738,7 +741,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)M * NH * HD * 2));
   const unsigned rec = ATT_REC;
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * rec * 4));
-  const int maxseg = ATT_QN / G;
+  const int maxseg = min(ATT_QN / G, ATT_MAXSEG);
   bool first_seg = true;
   // one 32-key block of K (S^T operand: lane = key l16 of half t, dims kb*32 + g4*8) and V
   // (rows of 16 keys x 8 dims, transposed through LDS below)
@@ -760,8 +763,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     }
   };
   // ---- a round's segments: (row, kv head) pairs whose blocks meet [i, i1), then the wave's
-  // first block of the round's first segment (its latency overlaps the prologue), unless it is
-  // the pair's newest block (whose key at pos the prologue writes)
+  // first block of the round's first segment (its latency overlaps the prologue)
   auto start_round = [&](int i) {
     if (tid() == 0) {
       int n = 0, u = i;
@@ -790,8 +792,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     bool pre = false;
     if (sh.nseg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
-      const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
-      pre = wave < ns && j0 + wave != ((Lb + 31) >> 5) - 1;
+      pre = wave < ns;
       if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
     }
     return pre;
@@ -803,8 +804,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     if (i != i0) pre = start_round(i);
     const int nsg = sh.nseg;
     const int inext = sh.segnext;
-    // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; the
-    // segment holding the newest block also writes K/V of position pos
+    // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; for the
+    // segment holding the newest block also k of position pos (normalised, rotated) and v
     for (int task = wave; task < nsg * (G + 2); task += NWAVE) {
       const int sg = task / (G + 2), tk = task - sg * (G + 2);
       const int b = sh.seg[sg][0], kvh = sh.seg[sg][1];
@@ -828,18 +829,11 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       const float s0 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(sinr, cb + lane * 2, 0, 0));
       const float s1 = bf2f((unsigned short)__builtin_amdgcn_raw_buffer_load_b16(sinr, cb + (lane + 64) * 2, 0, 0));
       if (tk <= G) head_norm_rope(a, x0, x1, w0, w1, c0, c1, s0, s1, pok);
-      if (tk < G) {
-        sh.u.a.qn[sg * G + tk][lane] = f2bf(x0);
-        sh.u.a.qn[sg * G + tk][lane + 64] = f2bf(x1);
-      } else {
-        const rsrc_t cr = tk == G ? kwr : vwr;
-        const unsigned co = (unsigned)(((size_t)(b * NKV + kvh) * a.cap + p0) * HD * 2);
-        stc_b16(cr, co + lane * 2, f2bf(x0));
-        stc_b16(cr, co + (lane + 64) * 2, f2bf(x1));
-      }
+      bf16* dst = tk < G ? sh.u.a.qn[sg * G + tk] : sh.u.a.kvn[2 * sg + (tk - G)];
+      dst[lane] = f2bf(x0);
+      dst[lane + 64] = f2bf(x1);
     }
-    __builtin_amdgcn_s_waitcnt(0);          // K/V at pos written through before anyone reads it
-    __syncthreads();
+    lds_barrier();
     if (first_seg) STEP_TRACE(p, 5);
     for (int sg = 0; sg < nsg; ++sg) {
       const int b = sh.seg[sg][0], kvh = sh.seg[sg][1], j0 = sh.seg[sg][2], nseg = sh.seg[sg][3];
@@ -849,6 +843,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       const int bk = b * NKV + kvh;
       const size_t kvbase = (size_t)bk * a.cap * HD;
       const int S = sh.units[b] + kvh * (att_ovh(M) + nblk);
+      // the pair's newest block, when it is in this segment and pos is valid: key pos comes from
+      // the prologue's k and v
+      const bool pok = p0 >= 0 && p0 < a.cap && p0 < a.rope_rows;
+      const int jnew = pok && j0 + nseg == nblk ? nblk - 1 : -1;
       // Q^T operand (rows = the G query heads of this kv head; rows >= G zero)
       u32x4 qreg[4];
 #pragma unroll
@@ -863,6 +861,19 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       for (int k = wave; k < nseg; k += NWAVE) {
         const int key0 = (j0 + k) * 32;
         if (!pre) load_block(kvbase, key0);
+        if (j0 + k == jnew) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+              if (key0 + t * 16 + l16 == (int)p0)
+                kreg[t][kb] = *(const u32x4*)&sh.u.a.kvn[2 * sg][kb * 32 + g4 * 8];
+#pragma unroll
+          for (int it = 0; it < 8; ++it) {
+            const int cc = it * 64 + lane;
+            if (key0 + (cc >> 4) == (int)p0) vreg[it] = *(const u32x4*)&sh.u.a.kvn[2 * sg + 1][(cc & 15) * 8];
+          }
+        }
         f32x4 sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -949,6 +960,12 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         sh.ls[wave][l16] = l_run;
       }
       __syncthreads();
+      // the cache's K/V at pos (read by later steps only; complete before the phase's barrier)
+      if (jnew >= 0 && tid() < 32) {
+        const unsigned co = (unsigned)(((size_t)bk * a.cap + p0) * HD * 2);
+        const int which = tid() >> 4, ch = tid() & 15;
+        stc_b128(which ? vwr : kwr, co + ch * 16, *(const u32x4*)&sh.u.a.kvn[2 * sg + which][ch * 8]);
+      }
       // a (row, kv head) whose blocks all lie in this workgroup is finished here; one split over
       // workgroups leaves (o, m, l) partials, combined by its last contributor to arrive
       const bool whole = j0 == 0 && nseg == nblk;
