@@ -213,12 +213,14 @@ constexpr int MAXL = 64;                      // layers
 constexpr int LFIELDS = 10;                   // layer-table fields the phases read
 constexpr int MAXH = 4096;                    // hidden size (norm weight staged in LDS)
 constexpr int ATT_MAXSEG = 8;                 // attention segments of one round
+constexpr int LGS_ROWS = 1024;                // GEMV output units per workgroup staged in LDS
 
 struct Shared {
   union {
     struct {                                  // GEMV phases
       float red[NWAVE][TMAX][256];            // per-wave partial tiles of a chunk
       float res[TMAX * 16][MAXM + 1];         // the chunk's reduced rows
+      bf16 lgs[MAXM][LGS_ROWS];               // outputs of the chunks before the last
     } g;
     struct {                                  // attention
       bf16 v[NWAVE][32][HD + 8];
@@ -292,10 +294,11 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
 // GEMV phases
 
 // This workgroup's share of one GEMV phase: units u0 .. u0 + nu of the matrix, nch chunks of up
-// to CAPU units, nbpc prefetch batches per chunk (every wave has nk / 8 k-steps), nb batches.
+// to CAPU units, nbpc prefetch batches per chunk (every wave has J = nk / 8 k-steps, wave w's
+// i-th being k-step w + 8 i; batch bb holds its k-steps bb KB .. bb KB + KB - 1), nb batches.
 struct Geo {
   rsrc_t wr;                         // the workgroup's weight region (all its chunks)
-  int K, nk, u0, nu, nch, nbpc, nb;
+  int K, nk, J, u0, nu, nch, nbpc, nb;
 };
 
 template <int KIND>
@@ -304,12 +307,13 @@ __device__ __forceinline__ Geo make_geo(const bf16* W, int nunits, int K) {
   Geo g;
   g.K = K;
   g.nk = K >> 5;
+  g.J = g.nk >> 3;
   const int u0 = part_lo(nunits, gridDim.x, blockIdx.x);
   const int u1 = part_lo(nunits, gridDim.x, blockIdx.x + 1);
   g.u0 = u0;
   g.nu = u1 - u0;
   g.nch = (g.nu + CAPU - 1) / CAPU;
-  g.nbpc = ((g.nk >> 3) + KB - 1) / KB;
+  g.nbpc = (g.J + KB - 1) / KB;
   g.nb = g.nch * g.nbpc;
   g.wr = make_rsrc(W + (size_t)u0 * UPR * K, (unsigned)((size_t)g.nu * UPR * K * 2));
   return g;
@@ -321,6 +325,18 @@ __device__ __forceinline__ int chunk_rows(const Geo& g, int ch) {
   return min(mat_CAPU(KIND), g.nu - ch * mat_CAPU(KIND)) * mat_UPR(KIND);
 }
 
+// A batch position (chunk, batch within it), advanced one batch at a time: the stream's hot
+// loop does no divisions.
+struct Cur {
+  int ch, bb;
+};
+__device__ __forceinline__ void advance(const Geo& g, Cur& c) {
+  if (++c.bb == g.nbpc) {
+    c.bb = 0;
+    ++c.ch;
+  }
+}
+
 // One prefetch batch of a wave: KB k-steps, each T weight tiles (MFMA A operands) and the
 // activation block (B operand: lane l = row l % 16, columns (l / 16) * 8 .. +8 of the k-step).
 template <int KIND>
@@ -329,43 +345,75 @@ struct Buf {
   u32x4 x[mat_KB(KIND)];
 };
 
-// Weight loads of batch bi (chunk bi / nbpc). Loads are unconditional buffer loads: a tile row
-// past the chunk, a k-step past K or a batch past the workgroup's share reads zeros without
-// memory traffic, so the compiler waits for each register on its own (vmcnt(n)).
+// Per-lane byte offsets of batch 0 of a chunk's weight tiles and of the activation blocks; batch
+// bb adds bb * step, passed as the loads' scalar offset. A lane whose row is past the chunk (or
+// past the M activation rows) holds an offset past every range: its loads read zeros without
+// memory traffic, unconditionally, so the compiler waits for each register on its own.
 template <int KIND>
-__device__ __forceinline__ void issue_w(const Geo& g, int bi, Buf<KIND>& b) {
+struct WOff {
+  unsigned o[mat_KB(KIND)][mat_T(KIND)];
+  unsigned step;
+};
+template <int KIND>
+struct XOff {
+  unsigned o[mat_KB(KIND)];
+  unsigned step;
+};
+
+template <int KIND>
+__device__ __forceinline__ void set_chunk(const Geo& g, int ch, WOff<KIND>& w) {
   constexpr int T = mat_T(KIND), KB = mat_KB(KIND), CAPU = mat_CAPU(KIND), UPR = mat_UPR(KIND);
   const int lane = tid() & 63, wave = wave_id();
-  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
-  const bool chok = ch < g.nch;
-  const int rows = chok ? chunk_rows<KIND>(g, ch) : 0;
+  const int rows = ch < g.nch ? chunk_rows<KIND>(g, ch) : 0;
   const unsigned cbase = (unsigned)(ch * CAPU * UPR) * (unsigned)g.K * 2u;
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    const int ks = wave + NWAVE * (bb * KB + kb);
-    const bool okk = chok && ks < g.nk;
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const int j = 16 * t + (lane & 15);
-      const bool ok = okk && j < rows;
-      b.w[kb][t] = __builtin_amdgcn_raw_buffer_load_b128(
-          g.wr, ok ? cbase + (unsigned)(ks * rows + j) * 64u + (unsigned)(lane >> 4) * 16u : OOB, 0,
-          CP_NT);
+      w.o[kb][t] = j < rows ? cbase + (unsigned)((wave + NWAVE * kb) * rows + j) * 64u +
+                                  (unsigned)(lane >> 4) * 16u
+                            : OOB;
     }
+  w.step = (unsigned)(NWAVE * KB * rows) * 64u;
+}
+
+template <int KIND>
+__device__ __forceinline__ XOff<KIND> make_xoff(int M) {
+  constexpr int KB = mat_KB(KIND);
+  const int lane = tid() & 63, wave = wave_id();
+  XOff<KIND> x;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+    x.o[kb] = (lane & 15) < M ? (unsigned)(((wave + NWAVE * kb) * M + (lane & 15)) * 64 + (lane >> 4) * 16)
+                              : OOB;
+  x.step = (unsigned)(NWAVE * KB * M) * 64u;
+  return x;
+}
+
+// Loads of batch bb of the chunk `w` describes; a k-step past K (in a chunk's last batch) reads
+// zeros (out-of-range offset).
+template <int KIND>
+__device__ __forceinline__ void issue_w(const Geo& g, const WOff<KIND>& w, int bb, Buf<KIND>& b) {
+  constexpr int T = mat_T(KIND), KB = mat_KB(KIND);
+  const unsigned so = (unsigned)bb * w.step;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const bool ok = bb * KB + kb < g.J;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      b.w[kb][t] = __builtin_amdgcn_raw_buffer_load_b128(g.wr, ok ? w.o[kb][t] : OOB, ok ? so : 0u, CP_NT);
   }
 }
 
 template <int KIND>
-__device__ __forceinline__ void issue_x(const Geo& g, rsrc_t xr, int M, int bi, Buf<KIND>& b) {
+__device__ __forceinline__ void issue_x(const Geo& g, rsrc_t xr, const XOff<KIND>& x, int bb, Buf<KIND>& b) {
   constexpr int KB = mat_KB(KIND);
-  const int lane = tid() & 63, wave = wave_id();
-  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
-  const bool chok = ch < g.nch && (lane & 15) < M;
+  const unsigned so = (unsigned)bb * x.step;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
-    const int ks = wave + NWAVE * (bb * KB + kb);
-    const bool ok = chok && ks < g.nk;
-    b.x[kb] = ldb128(xr, ok ? (unsigned)(((ks * M + (lane & 15)) * 32 + (lane >> 4) * 8) * 2) : OOB);
+    const bool ok = bb * KB + kb < g.J;
+    b.x[kb] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? x.o[kb] : OOB, ok ? so : 0u, 0);
   }
 }
 
@@ -380,23 +428,21 @@ __device__ __forceinline__ u32x4 norm8(u32x4 x, float r, u32x4 wv) {
 }
 
 template <int KIND, bool NORM>
-__device__ __forceinline__ void consume(const Geo& g, const Shared& sh, const Buf<KIND>& b, int bi,
+__device__ __forceinline__ void consume(const Geo& g, const Shared& sh, const Buf<KIND>& b, int bb,
                                         float r, f32x4 (&acc)[mat_T(KIND)]) {
   constexpr int T = mat_T(KIND), KB = mat_KB(KIND);
   const int lane = tid() & 63, wave = wave_id();
-  const int ch = bi / g.nbpc, bb = bi - ch * g.nbpc;
-  if (ch >= g.nch) return;
-  const int rows = chunk_rows<KIND>(g, ch);
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     u32x4 xv = b.x[kb];
     if (NORM) {
-      const int ks = min(wave + NWAVE * (bb * KB + kb), g.nk - 1);
+      const int ks = wave + NWAVE * min(bb * KB + kb, g.J - 1);
       xv = norm8(xv, r, *(const u32x4*)&sh.lnw[ks * 32 + (lane >> 4) * 8]);
     }
+    // tiles past the chunk's rows hold zeros (their loads were out of range): no guard, so
+    // the tiles' MFMAs issue back to back
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-      if (16 * t < rows) acc[t] = mfma16x16x32(b.w[kb][t], xv, acc[t]);
+    for (int t = 0; t < T; ++t) acc[t] = mfma16x16x32(b.w[kb][t], xv, acc[t]);
   }
 }
 
@@ -411,7 +457,7 @@ __device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
 
 // Reduce the waves' tiles of chunk ch and run its epilogue. oslot: QKV/SILU the layer, RES the
 // h slot written (its input is slot oslot - 1, preloaded per thread in hin).
-template <int KIND, int EPI>
+template <int KIND, int EPI, bool STAGE>
 __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& g, int ch,
                                           f32x4 (&acc)[mat_T(KIND)], int oslot, unsigned hin) {
   constexpr int T = mat_T(KIND), CAPU = mat_CAPU(KIND);
@@ -446,7 +492,8 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
     const rsrc_t qr = make_rsrc(qkv_slot(a, oslot), (unsigned)((size_t)M * nqkv * 2));
     for (int e = t; e < rows * M; e += NTHR) {
       const int m = e / rows, j = e - m * rows;
-      stc_b16(qr, (unsigned)((size_t)m * nqkv + r0 + j) * 2, f2bf(sh.u.g.res[j][m]));
+      if (STAGE) sh.u.g.lgs[m][ch * CAPU + j] = f2bf(sh.u.g.res[j][m]);
+      else stc_b16(qr, (unsigned)((size_t)m * nqkv + r0 + j) * 2, f2bf(sh.u.g.res[j][m]));
     }
   } else if (EPI == EPI_RES) {
     // residual columns ua .. ua + rows (<= 16): h[oslot] = bf16(h[oslot-1] + bf16(sum));
@@ -476,7 +523,8 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
       const float gv = rbf(sh.u.g.res[f][m]);
       const float uv = rbf(sh.u.g.res[nf + f][m]);
       const float s = rbf(gv / (1.0f + expf(-gv)));
-      stc_b16(mr, xoff(m, ua + f, M) * 2, f2bf(s * uv));
+      if (STAGE) sh.u.g.lgs[m][ch * CAPU + f] = f2bf(s * uv);
+      else stc_b16(mr, xoff(m, ua + f, M) * 2, f2bf(s * uv));
     }
   } else {
     // vocabulary rows ua .. ua + rows: logits out + the workgroup's running argmax per token
@@ -487,7 +535,8 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
       for (int j = v; j < rows; j += 32) {
         const bf16 bv = f2bf(sh.u.g.res[j][m]);
         const int col = r0 + j;
-        a.logits[(size_t)m * a.V + col] = bv;
+        if (STAGE) sh.u.g.lgs[m][ch * CAPU + j] = bv;   // written out after the stream
+        else a.logits[(size_t)m * a.V + col] = bv;
         const float fv = bf2f(bv);
         if (am_better(fv, col, val, idx)) {
           val = fv;
@@ -510,19 +559,65 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
   STEP_TRACE(a.phase_cur, 8);
 }
 
-// Consume batch bi from ring slot b, refill the slot with batch bi + NBUF, finish the chunk when
-// bi is its last batch.
-template <int KIND, bool NORM, int EPI>
-__device__ __forceinline__ void gemv_step(const Args& a, Shared& sh, const Geo& g, rsrc_t xr, Buf<KIND>& b,
-                                          int bi, float r, f32x4 (&acc)[mat_T(KIND)], int oslot,
-                                          unsigned hin) {
+// The refill side of a phase's weight stream: the next batch to request (rc) and the load
+// offsets of rc's chunk. Past the workgroup's share rc's chunk has no rows, so every load of a
+// request reads zeros without memory traffic: requests are unconditional.
+template <int KIND>
+struct Refill {
+  Cur rc;
+  int wch;                                   // chunk `wo` describes
+  WOff<KIND> wo;
+};
+
+// Request the next batch into ring slot b (weights, and the activation when `x`).
+template <int KIND>
+__device__ __forceinline__ void refill(const Geo& g, rsrc_t xr, const XOff<KIND>& xo, Refill<KIND>& f,
+                                       Buf<KIND>& b, bool x) {
+  if (f.rc.ch != f.wch) {                    // the next chunk (or none: past the share)
+    set_chunk<KIND>(g, f.rc.ch, f.wo);
+    f.wch = f.rc.ch;
+  }
+  issue_w<KIND>(g, f.wo, f.rc.bb, b);
+  if (x) issue_x<KIND>(g, xr, xo, f.rc.bb, b);
+  advance(g, f.rc);
+}
+
+// The batch loop of a GEMV phase: consume each batch from its ring slot and refill the slot with
+// the next batch to request. The loop holds no global store when the workgroup has one chunk
+// (MODE 0: its epilogue follows the loop) or stages its earlier chunks' outputs in LDS (MODE 1),
+// so the compiler waits for each ring register on its own (a global store in the loop would make
+// it wait for every load in flight instead).
+template <int KIND, bool NORM, int EPI, int MODE>
+__device__ __forceinline__ void stream_loop(const Args& a, Shared& sh, const Geo& g, rsrc_t xr,
+                                            const XOff<KIND>& xo, Refill<KIND>& f,
+                                            Buf<KIND> (&ring)[mat_NBUF(KIND)], float r,
+                                            f32x4 (&acc)[mat_T(KIND)], int oslot, unsigned hin) {
   constexpr int NBUF = mat_NBUF(KIND);
-  if (bi >= g.nb) return;
-  consume<KIND, NORM>(g, sh, b, bi, r, acc);
-  issue_w<KIND>(g, bi + NBUF, b);
-  issue_x<KIND>(g, xr, a.M, bi + NBUF, b);
-  __builtin_amdgcn_sched_barrier(0);          // keep the refill ahead of the next batch's MFMAs
-  if (bi % g.nbpc == g.nbpc - 1) chunk_end<KIND, EPI>(a, sh, g, bi / g.nbpc, acc, oslot, hin);
+  Cur cc = {0, 0};
+  auto step = [&](Buf<KIND>& b) {
+    consume<KIND, NORM>(g, sh, b, cc.bb, r, acc);
+    refill<KIND>(g, xr, xo, f, b, true);
+    __builtin_amdgcn_sched_barrier(0);        // keep the refill ahead of the next batch's MFMAs
+    if (MODE == 1 && cc.bb == g.nbpc - 1 && cc.ch + 1 < g.nch)
+      chunk_end<KIND, EPI, true>(a, sh, g, cc.ch, acc, oslot, hin);
+    advance(g, cc);
+  };
+  // the first round of the ring on its own (its activation loads went out after the other
+  // slots' weights), then whole rounds (every slot consumed: the loop's entry and back edge
+  // carry the same loads in flight, so each batch waits for its own registers only), then the
+  // remaining batches
+  int bi = 0;
+  if (g.nb >= NBUF) {
+#pragma unroll
+    for (int s = 0; s < NBUF; ++s) step(ring[s]);
+    for (bi = NBUF; bi + NBUF <= g.nb; bi += NBUF) {
+#pragma unroll
+      for (int s = 0; s < NBUF; ++s) step(ring[s]);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s)
+    if (bi + s < g.nb) step(ring[s]);
 }
 
 // One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, then
@@ -555,8 +650,13 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
         0, 0);
   }
   constexpr int NPRE = mat_NPRE(KIND);
+  Refill<KIND> f;
+  f.rc = Cur{0, 0};
+  f.wch = 0;
+  set_chunk<KIND>(g, 0, f.wo);
+  const XOff<KIND> xo = make_xoff<KIND>(M);
 #pragma unroll
-  for (int s = 0; s < NPRE; ++s) issue_w<KIND>(g, s, ring[s]);
+  for (int s = 0; s < NPRE; ++s) refill<KIND>(g, g.wr, xo, f, ring[s], false);   // weights only
   if (NORM && tid() * 8 < K) *(u32x4*)&sh.lnw[tid() * 8] = lw;
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
@@ -572,13 +672,16 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
       sv[i] = ldb128(ssr, q < (int)gridDim.x * 4 ? (unsigned)(q * 16) : OOB);
     }
   }
+  {
+    Cur xc = {0, 0};                         // the activation of the batches requested before the wait
 #pragma unroll
-  for (int s = 0; s < NPRE; ++s) issue_x<KIND>(g, xr, M, s, ring[s]);
-#pragma unroll
-  for (int s = NPRE; s < NBUF; ++s) {
-    issue_w<KIND>(g, s, ring[s]);
-    issue_x<KIND>(g, xr, M, s, ring[s]);
+    for (int s = 0; s < NPRE; ++s) {
+      issue_x<KIND>(g, xr, xo, xc.bb, ring[s]);
+      advance(g, xc);
+    }
   }
+#pragma unroll
+  for (int s = NPRE; s < NBUF; ++s) refill<KIND>(g, xr, xo, f, ring[s], true);
   float r = 0.f;
   if (NORM) {
     const int lane = tid() & 63, wave = wave_id();
@@ -610,9 +713,28 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
   f32x4 acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int bi = 0; bi < g.nb; bi += NBUF) {
-#pragma unroll
-    for (int s = 0; s < NBUF; ++s) gemv_step<KIND, NORM, EPI>(a, sh, g, xr, ring[s], bi + s, r, acc, oslot, hin);
+  if (EPI == EPI_RES) {                      // O / down: one chunk (H <= 16 G, checked)
+    stream_loop<KIND, NORM, EPI, 0>(a, sh, g, xr, xo, f, ring, r, acc, oslot, hin);
+    if (g.nch == 1) chunk_end<KIND, EPI, false>(a, sh, g, 0, acc, oslot, hin);
+  } else if (g.nch > 0) {
+    // several chunks (O / down have one: H <= 16 G): the earlier chunks' outputs are staged in
+    // LDS (at most LGS_ROWS units, checked on the host) and written out after the stream
+    stream_loop<KIND, NORM, EPI, 1>(a, sh, g, xr, xo, f, ring, r, acc, oslot, hin);
+    chunk_end<KIND, EPI, false>(a, sh, g, g.nch - 1, acc, oslot, hin);
+    const int R = (g.nch - 1) * mat_CAPU(KIND);           // staged units
+    for (int e = tid(); e < R * M; e += NTHR) {
+      const int m = e / R, j = e - m * R;
+      const bf16 v = sh.u.g.lgs[m][j];
+      if (EPI == EPI_LOGITS) {
+        a.logits[(size_t)m * a.V + g.u0 + j] = v;
+      } else if (EPI == EPI_QKV) {
+        const int nqkv = (a.NH + 2 * a.NKV) * HD;
+        stc_b16(make_rsrc(qkv_slot(a, oslot), (unsigned)((size_t)M * nqkv * 2)),
+                (unsigned)((size_t)m * nqkv + g.u0 + j) * 2, v);
+      } else {
+        stc_b16(make_rsrc(m_slot(a, oslot), (unsigned)((size_t)M * a.I * 2)), xoff(m, g.u0 + j, M) * 2, v);
+      }
+    }
   }
   if (EPI == EPI_RES && g.nch == 0 && tid() < MAXM) {   // no columns here: a zero partial
     const rsrc_t ssr = make_rsrc(ss_slot(a, oslot), (unsigned)(gridDim.x * MAXM * 4));
@@ -1333,6 +1455,11 @@ static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int 
     const long long units[5] = {(long long)(NH + 2 * NKV) * HD, H, I, H, V};
     for (int q = 0; q < 5; ++q)
       if (units[q] * G >= (1ll << 32)) return false;      // 32-bit partition arithmetic
+    // a workgroup's chunks before its last fit the LDS staging (QKV, gate/up, lm_head; O and
+    // down have one chunk)
+    if ((long long)((units[0] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_QKV)) return false;
+    if ((long long)((units[2] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_GU)) return false;
+    if ((long long)((units[4] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_LM)) return false;
     // a workgroup's weight region stays below 2^31 bytes (32-bit buffer offsets)
     if ((long long)((V + G - 1) / G) * H * 2 >= (1ll << 31)) return false;
     if ((long long)((I + G - 1) / G) * 2 * H * 2 >= (1ll << 31)) return false;
