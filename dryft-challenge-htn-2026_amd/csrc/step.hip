@@ -61,20 +61,22 @@ enum : int { M_QKV = 0, M_O = 1, M_GU = 2, M_D = 3, M_LM = 4, NMAT = 5 };
 #ifndef DD_KB_OD
 #define DD_KB_OD 8
 #endif
-#ifndef DD_NBUF
-#define DD_NBUF 2
-#endif
-#ifndef DD_NBUF_LM
-#define DD_NBUF_LM 2
-#endif
+// ring depths (measured per step at B = 16 / B = 1 against 2 slots everywhere: 3 slots for O,
+// gate/up, down and lm_head -4.1% / -3.6%; 4 for gate/up or O, or 3-4 for QKV, are slower)
 #ifndef DD_NBUF_QKV
-#define DD_NBUF_QKV DD_NBUF
+#define DD_NBUF_QKV 2
+#endif
+#ifndef DD_NBUF_O
+#define DD_NBUF_O 3
 #endif
 #ifndef DD_NBUF_GU
-#define DD_NBUF_GU 4
+#define DD_NBUF_GU 3
 #endif
 #ifndef DD_NBUF_D
-#define DD_NBUF_D DD_NBUF
+#define DD_NBUF_D 3
+#endif
+#ifndef DD_NBUF_LM
+#define DD_NBUF_LM 3
 #endif
 #ifndef DD_NPRE
 #define DD_NPRE 2
@@ -82,12 +84,12 @@ enum : int { M_QKV = 0, M_O = 1, M_GU = 2, M_D = 3, M_LM = 4, NMAT = 5 };
 __host__ __device__ constexpr int mat_T(int k) { return k == M_QKV ? 2 : k == M_GU ? 5 : k == M_LM ? 8 : 1; }
 __host__ __device__ constexpr int mat_KB(int k) { return k == M_QKV ? 2 : k == M_GU ? 1 : k == M_LM ? 1 : DD_KB_OD; }
 __host__ __device__ constexpr int mat_NBUF(int k) {
-  return k == M_LM ? DD_NBUF_LM : k == M_QKV ? DD_NBUF_QKV : k == M_GU ? DD_NBUF_GU : k == M_D ? DD_NBUF_D : DD_NBUF;
+  return k == M_LM ? DD_NBUF_LM : k == M_QKV ? DD_NBUF_QKV : k == M_GU ? DD_NBUF_GU : k == M_D ? DD_NBUF_D : DD_NBUF_O;
 }
 // Ring slots whose weight loads are issued before the barrier wait; the rest go out right after
 // it, so the stream continues while the activation and 1/rms loads are in flight. More slots
-// before the wait only delay the release (measured: gate/up 4 slots with 2 before the wait is
-// 0.5% faster per step than 2 slots, 3-4 slots all before it or 5-6 slots are slower).
+// before the wait only delay the release (measured: gate/up with all of 3-4 slots before the
+// wait is slower than 2 before it).
 __host__ __device__ constexpr int mat_NPRE(int k) { return mat_NBUF(k) < DD_NPRE ? mat_NBUF(k) : DD_NPRE; }
 #ifndef DD_OD_TILE
 #define DD_OD_TILE 0
