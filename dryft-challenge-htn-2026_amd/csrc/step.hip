@@ -90,7 +90,14 @@ __host__ __device__ constexpr int mat_NBUF(int k) {
 // it, so the stream continues while the activation and 1/rms loads are in flight. More slots
 // before the wait only delay the release (measured: gate/up with all of 3-4 slots before the
 // wait is slower than 2 before it).
-__host__ __device__ constexpr int mat_NPRE(int k) { return mat_NBUF(k) < DD_NPRE ? mat_NBUF(k) : DD_NPRE; }
+#ifndef DD_NPRE_D
+#define DD_NPRE_D DD_NPRE
+#endif
+#ifndef DD_NPRE_GU
+#define DD_NPRE_GU DD_NPRE
+#endif
+__host__ __device__ constexpr int mat_npre_max(int k) { return k == M_D ? DD_NPRE_D : k == M_GU ? DD_NPRE_GU : DD_NPRE; }
+__host__ __device__ constexpr int mat_NPRE(int k) { return mat_NBUF(k) < mat_npre_max(k) ? mat_NBUF(k) : mat_npre_max(k); }
 #ifndef DD_OD_TILE
 #define DD_OD_TILE 0
 #endif
@@ -912,8 +919,9 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     }
   };
   // ---- a round's segments: (row, kv head) pairs whose blocks meet [i, i1), then the wave's
-  // first block of the round's first segment (its latency overlaps the prologue)
-  auto start_round = [&](int i) {
+  // first block of the round's first segment (its latency overlaps the prologue; before the
+  // barrier wait wave 0, the poller, requests nothing so its poll is not queued behind a block)
+  auto start_round = [&](int i, bool before_wait) {
     if (tid() == 0) {
       int n = 0, u = i;
       while (u < i1 && n < maxseg) {
@@ -941,16 +949,16 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     bool pre = false;
     if (sh.nseg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
-      pre = wave < ns;
+      pre = wave < ns && !(before_wait && wave == 0);   // wave 0 polls the barrier
       if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
     }
     return pre;
   };
-  bool pre = start_round(i0);                // kreg/vreg hold the wave's next block
+  bool pre = start_round(i0, sync);                // kreg/vreg hold the wave's next block
   if (sync) bar_wait(a, sh, epoch);
   STEP_TRACE(p, 1);
   for (int i = i0; i < i1;) {
-    if (i != i0) pre = start_round(i);
+    if (i != i0) pre = start_round(i, false);
     const int nsg = sh.nseg;
     const int inext = sh.segnext;
     // ---- prologue for every segment of the round: q heads normalised + rotated into LDS; for the

@@ -198,17 +198,27 @@ def _close(got, want, what, rtol=2e-2, atol=2e-2):
     assert not bad.any(), (what, int(bad.sum()), d.max().item())
 
 
-@pytest.mark.parametrize("shape", ["qwen3", "small"])
+# widest geometry class the step takes on 256 CUs (H = 16 x 256, 8 query heads per kv head), with
+# more rows per workgroup than one chunk holds in QKV (40 > 32), gate/up (48 > 40 features) and
+# lm_head (157 > 128 rows): the earlier chunks' outputs go through the LDS staging
+WIDE = synth.qwen3_config(vocab_size=40000, hidden_size=4096, intermediate_size=12288,
+                          num_hidden_layers=1, num_attention_heads=64, num_key_value_heads=8,
+                          head_dim=128)
+
+
+@pytest.mark.parametrize("shape", ["qwen3", "small", "wide"])
 @torch.inference_mode()
 def test_fused_phases_per_kernel(cuda, shape):
     """Each phase of the one-launch step run on its own (phase_begin/phase_end) from the buffers
     the previous phase left, against the oracle's op on exactly those inputs (one layer, B=16
-    ragged positions; Qwen3-4B widths and the small geometry): per-kernel bf16 tolerance 2e-2,
-    the embedding gather bit-exact, K/V written exactly at pos."""
+    ragged positions; Qwen3-4B widths, the small and the wide geometry): per-kernel bf16
+    tolerance 2e-2, the embedding gather bit-exact, K/V written exactly at pos."""
     if shape == "qwen3":
         cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
-    else:
+    elif shape == "small":
         cfg = dict(SMALL, num_hidden_layers=1)
+    else:
+        cfg = WIDE
     V = cfg["vocab_size"]
     ref, eng = _engine(cfg, seed=12)
     ops, l, rl = ref.ops, eng.layers[0], ref.layers[0]
