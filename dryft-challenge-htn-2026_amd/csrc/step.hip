@@ -783,10 +783,13 @@ __device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& 
 }
 
 // The units are split over the first Ga workgroups, Ga = min(grid, T / ATT_MINU): a small
-// workload (short contexts, B = 1) stays on fewer workgroups, so a (row, kv head) is split over
-// few contributors. Partition arithmetic stays in 32 bits (units x workgroups < 2^31, checked
-// on the host).
-constexpr int ATT_MINU = 16;
+// workload (short contexts, B = 1) stays on fewer workgroups, at least ATT_MINU units each
+// (measured at B = 1: 8 is 2.3% faster per step than 16; 4-8 are equal). Partition arithmetic
+// stays in 32 bits (units x workgroups < 2^31, checked on the host).
+#ifndef DD_ATT_MINU
+#define DD_ATT_MINU 8
+#endif
+constexpr int ATT_MINU = DD_ATT_MINU;
 __device__ __forceinline__ int attn_owner(int T, int Ga, int i) {  // workgroup of global unit i
   return (int)(((unsigned)(i + 1) * Ga - 1) / (unsigned)T);
 }
@@ -797,9 +800,13 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 // Partition units of one (row, kv head): att_ovh(M) units for its fixed per-segment latency
 // (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
 // many short segments gets fewer blocks. With one or two rows the few pairs are spread over more
-// workgroups by a larger weight (measured: B = 1 2.32 vs 2.38 ms per step, B = 16 best at 12).
-constexpr int ATT_OVH_MAX = 24;
-__host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? ATT_OVH_MAX : 12; }
+// workgroups by a larger weight (B = 16 best at 12; at B = 1 any weight from 8 to 48 measures
+// the same with ATT_MINU 8).
+#ifndef DD_ATT_OVH_SMALL
+#define DD_ATT_OVH_SMALL 24
+#endif
+constexpr int ATT_OVH_MAX = DD_ATT_OVH_SMALL > 12 ? DD_ATT_OVH_SMALL : 12;
+__host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? DD_ATT_OVH_SMALL : 12; }
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
