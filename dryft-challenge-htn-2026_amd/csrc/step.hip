@@ -805,8 +805,11 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 #ifndef DD_ATT_OVH_SMALL
 #define DD_ATT_OVH_SMALL 24
 #endif
-constexpr int ATT_OVH_MAX = DD_ATT_OVH_SMALL > 12 ? DD_ATT_OVH_SMALL : 12;
-__host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? DD_ATT_OVH_SMALL : 12; }
+#ifndef DD_ATT_OVH
+#define DD_ATT_OVH 12
+#endif
+constexpr int ATT_OVH_MAX = DD_ATT_OVH_SMALL > DD_ATT_OVH ? DD_ATT_OVH_SMALL : DD_ATT_OVH;
+__host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? DD_ATT_OVH_SMALL : DD_ATT_OVH; }
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
@@ -1472,11 +1475,14 @@ static bool geometry_ok(int L, int H, int NH, int NKV, int I, int V, int M, int 
     const long long units[5] = {(long long)(NH + 2 * NKV) * HD, H, I, H, V};
     for (int q = 0; q < 5; ++q)
       if (units[q] * G >= (1ll << 32)) return false;      // 32-bit partition arithmetic
-    // a workgroup's chunks before its last fit the LDS staging (QKV, gate/up, lm_head; O and
-    // down have one chunk)
-    if ((long long)((units[0] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_QKV)) return false;
-    if ((long long)((units[2] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_GU)) return false;
-    if ((long long)((units[4] + G - 1) / G) > LGS_ROWS + mat_CAPU(M_LM)) return false;
+    // a workgroup's chunks before its last fit the LDS staging: (chunks - 1) x chunk units <=
+    // LGS_ROWS for QKV, gate/up and lm_head (O and down have one chunk)
+    const int stq[3] = {M_QKV, M_GU, M_LM};
+    for (int q = 0; q < 3; ++q) {
+      const long long cap = mat_CAPU(stq[q]);
+      const long long nu = (units[stq[q]] + G - 1) / G;          // most units of a workgroup
+      if (((nu + cap - 1) / cap - 1) * cap > LGS_ROWS) return false;
+    }
     // a workgroup's weight region stays below 2^31 bytes (32-bit buffer offsets)
     if ((long long)((V + G - 1) / G) * H * 2 >= (1ll << 31)) return false;
     if ((long long)((I + G - 1) / G) * 2 * H * 2 >= (1ll << 31)) return false;

@@ -15,6 +15,7 @@ import math
 import pytest
 import torch
 
+import dryft_amd
 from dryft_amd import synth
 from oracle.reference import OracleEngine
 
@@ -162,6 +163,20 @@ def test_fused_step_unsupported_geometry(cuda):
     eng = Engine.from_state_dict(tiny, {k: v.cuda() for k, v in w.items()}, selftest=False)
     assert eng.step is None
     assert eng._new_state(2, 128).fused is None
+
+
+def test_fused_step_staging_limit(cuda):
+    """dd_step_supported takes a GEMV with several chunks per workgroup only while the chunks
+    before the last fit the LDS staging (1,024 output units): gate/up chunks hold 40 features,
+    so on 256 workgroups 1,040 features each (26 chunks) are taken and 1,041 (27) are not."""
+    L = dryft_amd.lib()
+    G = L.dd_step_grid()
+    if G != 256:
+        pytest.skip(f"limits computed for 256 workgroups, device has {G}")
+    ok = lambda I, V=151936: L.dd_step_supported(1, 2560, 32, 8, I, V, 16)
+    assert ok(1040 * 256) == 1 and ok(1040 * 256 + 256) == 0
+    # lm_head: 128-row chunks, 1,024 + 128 rows per workgroup at most
+    assert ok(9728, V=1152 * 256) == 1 and ok(9728, V=1152 * 256 + 1) == 0
 
 
 def test_fused_step_qwen3_width_b16(cuda):
