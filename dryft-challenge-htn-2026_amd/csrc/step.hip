@@ -98,14 +98,8 @@ __host__ __device__ constexpr int mat_NBUF(int k) {
 #endif
 __host__ __device__ constexpr int mat_npre_max(int k) { return k == M_D ? DD_NPRE_D : k == M_GU ? DD_NPRE_GU : DD_NPRE; }
 __host__ __device__ constexpr int mat_NPRE(int k) { return mat_NBUF(k) < mat_npre_max(k) ? mat_NBUF(k) : mat_npre_max(k); }
-#ifndef DD_OD_TILE
-#define DD_OD_TILE 0
-#endif
-// O / down: units of 16 contiguous rows (whole MFMA tiles, on H / 16 workgroups) when
-// DD_OD_TILE, else single rows (H / G rows on every workgroup)
-__host__ __device__ constexpr int mat_UPR(int k) {
-  return k == M_GU ? 2 : (DD_OD_TILE && (k == M_O || k == M_D)) ? 16 : 1;
-}
+// weight rows per partition unit: gate/up 2 (a feature's gate and up rows), else 1
+__host__ __device__ constexpr int mat_UPR(int k) { return k == M_GU ? 2 : 1; }
 __host__ __device__ constexpr int mat_CAPU(int k) { return mat_T(k) * 16 / mat_UPR(k); }
 constexpr int TMAX = 8;
 
@@ -1253,7 +1247,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
                                        uniform_ptr<const bf16>(lp[F_LN1]), ss_slot(a, 2 * layer), layer);
         break;
       case P_O:
-        run_gemv<M_O, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WO]), a.H / mat_UPR(M_O),
+        run_gemv<M_O, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WO]), a.H,
                                       a.NH * HD, attn_slot(a, layer), nullptr, nullptr, 2 * layer + 1);
         break;
       case P_GU:
@@ -1263,7 +1257,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
                                        layer);
         break;
       case P_D:
-        run_gemv<M_D, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WD]), a.H / mat_UPR(M_D),
+        run_gemv<M_D, false, EPI_RES>(a, sh, p, sync, epoch, uniform_ptr<const bf16>(lp[F_WD]), a.H,
                                       a.I, m_slot(a, layer), nullptr, nullptr, 2 * layer + 2);
         break;
       case P_LM:
@@ -1342,7 +1336,7 @@ __global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restric
   const int q8 = K >> 3;
   if (idx >= (size_t)N * q8) return;
   const int r = (int)(idx / q8), q = (int)(idx - (size_t)r * q8);
-  const int UPR = kind == M_GU ? 2 : kind == M_O ? mat_UPR(M_O) : kind == M_D ? mat_UPR(M_D) : 1;
+  const int UPR = kind == M_GU ? 2 : 1;
   const int CAPU = kind == M_QKV ? mat_CAPU(M_QKV) : kind == M_O ? mat_CAPU(M_O)
                  : kind == M_GU ? mat_CAPU(M_GU) : kind == M_D ? mat_CAPU(M_D) : mat_CAPU(M_LM);
   const bool gu = kind == M_GU;
