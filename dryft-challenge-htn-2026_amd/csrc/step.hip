@@ -190,8 +190,29 @@ __device__ __forceinline__ bf16* h_slot(const Args& a, int k) {
 __device__ __forceinline__ float* ss_slot(const Args& a, int k) {
   return a.ws + a.off_ss + (size_t)k * gridDim.x * MAXM;
 }
+// The raw q|k|v slot is head-grouped: row m holds, per kv head h, its G = NH / NKV q heads, then
+// k head h, then v head h (128 columns each), so one kv head's projection is a contiguous range
+// of QKV rows (dd_tile_weight lays the QKV weight out in the same row order).
 __device__ __forceinline__ bf16* qkv_slot(const Args& a, int l) {
   return a.qkv + (size_t)l * a.M * (a.NH + 2 * a.NKV) * HD;
+}
+
+// XCD-local QKV -> attention hand-off. With a multiple of 8 kv heads (and of 8 workgroups), XCD x
+// (workgroups c with c % 8 == x) computes the QKV rows of kv heads [x NKV / 8, (x + 1) NKV / 8)
+// and runs the attention of exactly those heads, so the attention phase waits for its own XCD's
+// arrivals only: 8 attention groups (measured at B = 16: 1.0% per step). With fewer than
+// DD_ATT_XCD_MINM rows an XCD's attention is one or two (row, head) pairs on a few workgroups and
+// the local wait measured no gain (B = 1: 0.5% slower), so those steps, and geometries without a
+// multiple of 8 kv heads, use one group (every workgroup, every head) and the full barrier. The
+// choice depends only on the launch's arguments, so the QKV and attention phases agree on it.
+#ifndef DD_ATT_XCD
+#define DD_ATT_XCD 1
+#endif
+#ifndef DD_ATT_XCD_MINM
+#define DD_ATT_XCD_MINM 3
+#endif
+__device__ __forceinline__ int att_groups(const Args& a) {
+  return DD_ATT_XCD && a.M >= DD_ATT_XCD_MINM && (a.NKV & 7) == 0 && (gridDim.x & 7) == 0 ? 8 : 1;
 }
 __device__ __forceinline__ bf16* attn_slot(const Args& a, int l) {
   return a.attn + (size_t)l * a.M * a.NH * HD;
@@ -270,16 +291,19 @@ __device__ __forceinline__ void bar_arrive(const Args& a, unsigned epoch) {
 
 // Released when every XCD's counter has all its workgroups' arrivals: lanes 0..7 of wave 0 read
 // the 8 counters in one load, so the release is one memory latency after the last arrival.
-__device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epoch) {
+// xcd_local: only this workgroup's XCD's arrivals are waited for.
+__device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epoch,
+                                         bool xcd_local = false) {
   if (wave_id() == 0 && !sh.bail) {
     const int lane = tid() & 63;
     const unsigned target = epoch * (unsigned)(gridDim.x >> 3);
     const rsrc_t cr = make_rsrc(a.ctr + C_BAR, 9 * 64 * 4);
-    const unsigned off = lane < 8 ? (unsigned)(64 * (1 + lane) * 4) : 0xfffffff0u;
+    const bool mine = lane < 8 && (!xcd_local || lane == (int)(blockIdx.x & 7));
+    const unsigned off = mine ? (unsigned)(64 * (1 + lane) * 4) : 0xfffffff0u;
     const unsigned long long t0 = wall_clock64();
     for (;;) {
       const unsigned v = ldc_u32(cr, off);
-      if (__all(lane >= 8 || v >= target)) break;
+      if (__all(!mine || v >= target)) break;
       __builtin_amdgcn_s_sleep(DD_BAR_SLEEP);
       if (wall_clock64() - t0 > 20000000ull) {  // 200 ms: report, stop waiting from now on
         if (lane == 0) {
@@ -305,14 +329,14 @@ struct Geo {
 };
 
 template <int KIND>
-__device__ __forceinline__ Geo make_geo(const bf16* W, int nunits, int K) {
+__device__ __forceinline__ Geo make_geo(const bf16* W, int nunits, int K, int c) {
   constexpr int UPR = mat_UPR(KIND), CAPU = mat_CAPU(KIND), KB = mat_KB(KIND);
   Geo g;
   g.K = K;
   g.nk = K >> 5;
   g.J = g.nk >> 3;
-  const int u0 = part_lo(nunits, gridDim.x, blockIdx.x);
-  const int u1 = part_lo(nunits, gridDim.x, blockIdx.x + 1);
+  const int u0 = part_lo(nunits, gridDim.x, c);
+  const int u1 = part_lo(nunits, gridDim.x, c + 1);
   g.u0 = u0;
   g.nu = u1 - u0;
   g.nch = (g.nu + CAPU - 1) / CAPU;
@@ -634,7 +658,13 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
                                          const bf16* lnw, const float* ss, int oslot) {
   constexpr int T = mat_T(KIND), NBUF = mat_NBUF(KIND);
   constexpr int NSV = MAXG * 4 / NTHR;       // 16-byte sums-of-squares items per thread
-  const Geo g = make_geo<KIND>(W, nunits, K);
+  // partition index: the QKV phase of 8 attention groups gives XCD x the indices
+  // x G / 8 .. (x + 1) G / 8 - 1, whose units are its kv heads' rows (head-grouped, so
+  // part_lo(n, G, x G / 8) = x n / 8 is a head boundary)
+  const int c = KIND == M_QKV && att_groups(a) == 8
+                    ? (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3))
+                    : (int)blockIdx.x;
+  const Geo g = make_geo<KIND>(W, nunits, K, c);
   const int M = a.M;
   Buf<KIND> ring[NBUF];
   STEP_TRACE(p, 0);
@@ -819,7 +849,7 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
         atomicOr(a.err, E_POS);
       const int Lb = (int)min<int64_t>(max<int64_t>(p + 1, 0), (int64_t)a.cap);
       const int nblk = (Lb + 31) >> 5;
-      cnt = nblk > 0 ? a.NKV * (att_ovh(a.M) + nblk) : 0;
+      cnt = nblk > 0 ? a.NKV / att_groups(a) * (att_ovh(a.M) + nblk) : 0;
     }
     int inc = cnt;
 #pragma unroll
@@ -830,9 +860,9 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
     if (b <= a.M) sh.units[b] = inc - cnt;   // lane M: cnt = 0, inc = total
   }
   __syncthreads();
-  const int T = sh.units[a.M];
-  const int Ga = max(1, min((int)gridDim.x, T / ATT_MINU));
-  for (int c = tid(); c <= (int)gridDim.x; c += NTHR) sh.afirst[c] = attn_first(T, Ga, c);
+  const int T = sh.units[a.M], Gl = (int)gridDim.x / att_groups(a);
+  const int Ga = max(1, min(Gl, T / ATT_MINU));
+  for (int c = tid(); c <= Gl; c += NTHR) sh.afirst[c] = attn_first(T, Ga, c);
   if (tid() == 0) sh.aG = Ga;
   __syncthreads();
 }
@@ -841,7 +871,7 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
 // (in workgroup order) into the bf16 attention output; run by the last contributor to arrive.
 // Pair start S: a contributor's record is its slot 0 when the pair is its first segment.
 __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, int layer, int b,
-                                             int kvh, int S, int fw, int lw) {
+                                             int kvh, int S, int fw, int lw, int P, int gx) {
   const int NH = a.NH, G = a.NH / a.NKV;
   const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * G * ATT_REC * 4));
   const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)a.M * NH * HD * 2));
@@ -855,7 +885,8 @@ __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, in
         const int c = c0 + j;
         const bool ok = c <= lw && sh.afirst[c + 1] > sh.afirst[c];
         const unsigned ro =
-            ok ? (unsigned)(((c * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G + row) * ATT_REC) * 4 : OOB;
+            ok ? (unsigned)((((c * P + gx) * 2 + (sh.afirst[c] >= S ? 0 : 1)) * G + row) * ATT_REC) * 4
+               : OOB;
         mv[j] = ok ? ldc_f32(pr, ro + HD * 4) : -INFINITY;
         lv[j] = ldc_f32(pr, ok ? ro + (HD + 1) * 4 : OOB);
         ov[j] = ldc_f32(pr, ok ? ro + d * 4 : OOB);
@@ -890,7 +921,11 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   const int nqkv = (NH + 2 * NKV) * HD;
   const float scale_log2 = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
   STEP_TRACE(p, 4);
-  const int i0 = sh.afirst[blockIdx.x], i1 = sh.afirst[blockIdx.x + 1];
+  // attention group gx of P (XCD gx when P = 8) takes kv heads h0 .. h0 + NKV / P - 1; the
+  // partition (sh.units, sh.afirst) is over its heads and its workgroups li = 0 .. G / P - 1
+  const int P = att_groups(a), gx = (int)blockIdx.x % P, li = (int)blockIdx.x / P;
+  const int h0 = gx * (NKV / P);
+  const int i0 = sh.afirst[li], i1 = sh.afirst[li + 1];
   const int Tu = sh.units[M], Ga = sh.aG;
   const unsigned kvbytes = (unsigned)((size_t)M * NKV * a.cap * HD * 2);
   const rsrc_t kwr = make_rsrc(kc, kvbytes), vwr = make_rsrc(vc, kvbytes);
@@ -934,8 +969,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         const int Lb = (int)min<int64_t>(max<int64_t>(sh.posv[b] + 1, 0), (int64_t)a.cap);
         const int nblk = (Lb + 31) >> 5;
         const int per = att_ovh(M) + nblk;
-        const int kvh = (u - sh.units[b]) / per;
-        const int S = sh.units[b] + kvh * per;                      // pair start (overhead units)
+        const int kvh = h0 + (u - sh.units[b]) / per;
+        const int S = sh.units[b] + (kvh - h0) * per;               // pair start (overhead units)
         const int lo = max(u, S + att_ovh(M)), hi = min(i1, S + per);
         if (hi > lo) {
           sh.seg[n][0] = b;
@@ -959,7 +994,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     return pre;
   };
   bool pre = start_round(i0, sync);                // kreg/vreg hold the wave's next block
-  if (sync) bar_wait(a, sh, epoch);
+  if (sync) bar_wait(a, sh, epoch, P == 8);
   STEP_TRACE(p, 1);
   for (int i = i0; i < i1;) {
     if (i != i0) pre = start_round(i, false);
@@ -975,7 +1010,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       const bool newest = sh.seg[sg][2] + sh.seg[sg][3] == ((Lb + 31) >> 5);
       const bool pok = p0 >= 0 && p0 < a.cap && p0 < a.rope_rows;
       if (tk >= G && !(newest && pok)) continue;
-      const int col = tk < G ? (kvh * G + tk) * HD : tk == G ? (NH + kvh) * HD : (NH + NKV + kvh) * HD;
+      const int col = (kvh * (G + 2) + tk) * HD;   // head-grouped: q heads, k, v
       const unsigned ro = (unsigned)((size_t)b * nqkv + col) * 2;
       // every load of the task is issued before the first use (one memory latency): raw head,
       // norm weight, cos/sin row (row 0 stands in for an invalid position)
@@ -1003,7 +1038,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       const int nblk = (Lb + 31) >> 5;
       const int bk = b * NKV + kvh;
       const size_t kvbase = (size_t)bk * a.cap * HD;
-      const int S = sh.units[b] + kvh * (att_ovh(M) + nblk);
+      const int S = sh.units[b] + (kvh - h0) * (att_ovh(M) + nblk);
       // the pair's newest block, when it is in this segment and pos is valid: key pos comes from
       // the prologue's k and v
       const bool pok = p0 >= 0 && p0 < a.cap && p0 < a.rope_rows;
@@ -1162,7 +1197,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         int nc = 0;
         for (int c = fw; c <= lw; ++c) nc += sh.afirst[c + 1] > sh.afirst[c];
         if (arrive_last(a.ctr + C_ATT + bk, nc, &sh.flag))
-          attn_combine(a, sh, layer, b, kvh, S, fw, lw);
+          attn_combine(a, sh, layer, b, kvh, S, fw, lw, P, gx);
       }
       __syncthreads();
     }
@@ -1329,13 +1364,24 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
 // workgroups exactly as the step's GEMV phases split it; workgroup c's units are stored from
 // unit u0(c) on (so its region starts at byte u0 * UPR * K * 2), in chunks of up to CAPU units;
 // a chunk of `rows` weight rows (gate rows, then up rows) is k-step-major: row j of k-step ks
-// (32 columns, 64 bytes) at chunk byte (ks * rows + j) * 64.
+// (32 columns, 64 bytes) at chunk byte (ks * rows + j) * 64. QKV rows are taken in head-grouped
+// order (aux = NKV kv heads): row r of kv head h = r / per (per = N / NKV rows) is q row
+// h G HD + t for t = r % per < G HD, else k row (NH + h) HD + t - G HD, else v row
+// (NH + NKV + h) HD + t - (G + 1) HD of cat(q, k, v). Gate/up: aux = I.
 __global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst, int N, int K,
-                                   int kind, int gate_up_I, int G) {
+                                   int kind, int aux, int G) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   const int q8 = K >> 3;
   if (idx >= (size_t)N * q8) return;
   const int r = (int)(idx / q8), q = (int)(idx - (size_t)r * q8);
+  int sr = r;                                               // source row of tiled-order row r
+  if (kind == M_QKV) {
+    const int per = N / aux, Gq = per / HD - 2, h = r / per, t = r - h * per, NHq = aux * Gq;
+    sr = t < Gq * HD ? h * Gq * HD + t
+       : t < (Gq + 1) * HD ? (NHq + h) * HD + t - Gq * HD
+                           : (NHq + aux + h) * HD + t - (Gq + 1) * HD;
+  }
+  const int gate_up_I = kind == M_GU ? aux : 0;
   const int UPR = kind == M_GU ? 2 : 1;
   const int CAPU = kind == M_QKV ? mat_CAPU(M_QKV) : kind == M_O ? mat_CAPU(M_O)
                  : kind == M_GU ? mat_CAPU(M_GU) : kind == M_D ? mat_CAPU(M_D) : mat_CAPU(M_LM);
@@ -1352,7 +1398,7 @@ __global__ void tile_weight_kernel(const bf16* __restrict__ src, bf16* __restric
   const int j = gu ? (u - ua) + (half ? nu : 0) : r - ua * UPR;
   const int ks = q >> 2, kq = q & 3;
   const size_t d = (size_t)ua * UPR * K + ((size_t)ks * rows + j) * 32 + kq * 8;
-  *(u32x4*)(dst + d) = *(const u32x4*)(src + (size_t)r * K + q * 8);
+  *(u32x4*)(dst + d) = *(const u32x4*)(src + (size_t)sr * K + q * 8);
 }
 
 }  // namespace st
@@ -1436,11 +1482,12 @@ DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV) {
 
 DD_API size_t dd_tiled_bytes(int N, int K) { return (size_t)N * K * 2; }
 
-DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gate_up_I,
+DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int aux,
                           hipStream_t stream) {
   DD_REQUIRE(src && dst && matrix >= 0 && matrix < NMAT && N >= 1 && K >= 256 && K % 256 == 0);
-  DD_REQUIRE((matrix == M_GU) == (gate_up_I > 0));
-  DD_REQUIRE(gate_up_I == 0 || N == 2 * gate_up_I);
+  DD_REQUIRE((matrix == M_GU || matrix == M_QKV) == (aux > 0));
+  DD_REQUIRE(matrix != M_GU || N == 2 * aux);
+  DD_REQUIRE(matrix != M_QKV || (N % aux == 0 && (N / aux) % HD == 0 && N / aux >= 3 * HD));
   DD_REQUIRE(aligned16(src) && aligned16(dst));
   DD_REQUIRE((long long)N * K < (1ll << 40));
   int G = 0;
@@ -1449,7 +1496,7 @@ DD_API int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, 
   DD_REQUIRE((long long)N * G < (1ll << 32));
   const size_t n16 = (size_t)N * (K / 8);
   hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, stream,
-                     (const bf16*)src, (bf16*)dst, N, K, matrix, gate_up_I, G);
+                     (const bf16*)src, (bf16*)dst, N, K, matrix, aux, G);
   return launch_status();
 }
 

@@ -45,23 +45,35 @@ class FusedStep:
         self.I = e.layers[0].wd.shape[1]
         if not self.L.dd_step_supported(e.L, self.H, e.nh, e.nkv, self.I, self.V, MAXM):
             raise RuntimeError("dd_step_supported: model geometry not taken by the fused step")
-        # matrix kinds of dd_tile_weight: 0 wqkv, 1 wo, 2 wgu, 3 wd, 4 lm_head (each laid out
-        # for the workgroup split of its GEMV phase on this device)
+        # matrix kinds of dd_tile_weight: 0 wqkv (rows head-grouped: aux = kv heads), 1 wo,
+        # 2 wgu (aux = I), 3 wd, 4 lm_head (each laid out for the workgroup split of its GEMV
+        # phase on this device)
         with torch.no_grad():
             for l in e.layers:
-                l.wqkv_t = self._tile(l.wqkv, 0)
+                l.wqkv_t = self._tile(l.wqkv, 0, aux=e.nkv)
                 l.wo_t = self._tile(l.wo, 1)
-                l.wgu_t = self._tile(l.wgu, 2, gate_up_I=self.I)
+                l.wgu_t = self._tile(l.wgu, 2, aux=self.I)
                 l.wd_t = self._tile(l.wd, 3)
             self.lm_t = self._tile(e.lm_head, 4)
         torch.cuda.synchronize(e.dev)
 
-    def _tile(self, w, matrix, gate_up_I=0):
+    def _tile(self, w, matrix, aux=0):
         N, K = w.shape
         out = torch.empty(self.L.dd_tiled_bytes(N, K) // 2, dtype=torch.bfloat16, device=w.device)
-        check(self.L.dd_tile_weight(w.data_ptr(), out.data_ptr(), N, K, matrix, gate_up_I,
+        check(self.L.dd_tile_weight(w.data_ptr(), out.data_ptr(), N, K, matrix, aux,
                                     _stream(w.device)), "dd_tile_weight")
         return out
+
+    @staticmethod
+    def qkv_natural(x, nh, nkv):
+        """A head-grouped raw projection (last dim: per kv head its nh / nkv q heads, k, v; the
+        step's qkv slot) in the reference's cat(q, k, v) column order."""
+        g = nh // nkv
+        t = x.unflatten(-1, (nkv, g + 2, HD))
+        q = t[..., :g, :].flatten(-3)
+        k = t[..., g, :].flatten(-2)
+        v = t[..., g + 1, :].flatten(-2)
+        return torch.cat([q, k, v], dim=-1)
 
     @staticmethod
     def supports(B, W):
@@ -76,7 +88,8 @@ class FusedStep:
         f = _State()
         L = e.L
         # write-once activation slots (see dd_decode_step): h per producing phase, the others
-        # per layer; h, attn and mbuf slots are k-step-major ([K/32][B][32]), qkv row-major
+        # per layer; h, attn and mbuf slots are k-step-major ([K/32][B][32]), qkv row-major and
+        # head-grouped (qkv_natural)
         f.h = torch.empty(2 * L + 1, B, H, **bf)
         f.qkv = torch.empty(L, B, (e.nh + 2 * e.nkv) * HD, **bf)
         f.attn = torch.empty(L, B, e.nh * HD, **bf)

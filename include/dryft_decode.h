@@ -130,9 +130,11 @@ size_t dd_argmax_ws_bytes(int M, int V);
  * timeout that sets err flag 4 instead of hanging.
  *
  * Weights are streamed from a tiled copy made once per matrix by dd_tile_weight (the natural
- * row-major matrices stay the interface). matrix: 0 wqkv, 1 wo, 2 wgu (gate_up_I = I, N = 2 I),
- * 3 wd, 4 lm_head. The matrix is split into units (rows; wgu: features, unit u = gate row u and
- * up row I + u) over the dd_step_grid() workgroups, workgroup c taking units
+ * row-major matrices stay the interface). matrix: 0 wqkv (aux = NKV; rows taken head-grouped:
+ * per kv head h its NH / NKV q heads' rows, then k row block h, then v row block h, of cat(q, k,
+ * v)), 1 wo, 2 wgu (aux = I, N = 2 I), 3 wd, 4 lm_head (aux = 0 for 1, 3, 4). The matrix is split
+ * into units (rows; wgu: features, unit u = gate row u and up row I + u) over the
+ * dd_step_grid() workgroups, workgroup c taking units
  * [floor(n c / G), floor(n (c + 1) / G)); a workgroup's units are stored in order from byte
  * u0 * rows_per_unit * K * 2 on, in chunks of up to 32 / 16 / 40 / 16 / 128 units (per matrix as
  * listed); a chunk of R weight rows (wgu: its gate rows, then its up rows) is k-step-major: the
@@ -154,7 +156,7 @@ int dd_step_counters_alloc(void** out);
 int dd_step_counters_read(const void* counters, int* host);
 size_t dd_step_ws_bytes(int L, int NH, int NKV);
 size_t dd_tiled_bytes(int N, int K);
-int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gate_up_I,
+int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int aux,
                    hipStream_t stream);
 
 /* layer_table: [L][16] int64 device pointers per layer: 0 wqkv (tiled), 1 wo (tiled),
@@ -164,7 +166,8 @@ int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int gat
  * Activation buffers (bf16), written once per launch (one slot per producing phase, so they
  * are read with plain cached loads): h [2L+1] slots of M x H (slot 0 embedding, 2l+1 after layer
  * l's O projection, 2l+2 after its down projection), qkv [L, M, (NH + 2 NKV) * 128] (raw q|k|v
- * projection, row-major), attn [L] slots of M x NH*128, mbuf [L] slots of M x I; the h, attn and
+ * projection, row-major, head-grouped: [NKV][NH / NKV + 2][128] per row, a kv head's q heads
+ * then its k and v), attn [L] slots of M x NH*128, mbuf [L] slots of M x I; the h, attn and
  * mbuf slots are k-step-major: element (m, k) of a slot at ((k / 32) * M + m) * 32 + k % 32.
  * logits [M, V] (row-major) hold the step's lm_head output afterwards. ws: dd_step_ws_bytes; counters: dd_step_counters() zeroed ints.
  * phase_begin/phase_end select a sub-range of the 2 + 5L phases (0 embedding, 1 + 5l + {0 QKV,

@@ -49,20 +49,24 @@ def test_validation_rejects_without_launch():
                             1, 9, 32, 8, 128, 128, 128, None) == INVALID         # W*G > 32
     assert L.dd_attn_decode(fake, fake, fake, fake, 0, fake, fake, fake,
                             1, 1, 32, 8, 128, 128, 100, None) == INVALID         # chunk % 32
-    # weight tiling: matrix 0..4, K a multiple of 256, gate_up_I > 0 exactly for matrix 2 with
-    # N = 2 * gate_up_I
+    # weight tiling: matrix 0..4, K a multiple of 256; aux = I > 0 for matrix 2 with N = 2 I;
+    # aux = kv heads > 0 for matrix 0 with N / aux a whole number (>= 3) of 128-row heads
     assert L.dd_tile_weight(fake, fake, 64, 256, 5, 0, None) == INVALID
     assert L.dd_tile_weight(fake, fake, 64, 256, -1, 0, None) == INVALID
-    assert L.dd_tile_weight(fake, fake, 64, 384, 0, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 768, 384, 0, 1, None) == INVALID
     assert L.dd_tile_weight(fake, fake, 64, 256, 2, 0, None) == INVALID
     assert L.dd_tile_weight(fake, fake, 64, 256, 2, 48, None) == INVALID
     assert L.dd_tile_weight(fake, fake, 64, 256, 1, 32, None) == INVALID
-    assert L.dd_tile_weight(None, fake, 64, 256, 0, 0, None) == INVALID
+    assert L.dd_tile_weight(fake, fake, 768, 256, 0, 0, None) == INVALID      # no kv heads
+    assert L.dd_tile_weight(fake, fake, 768, 256, 0, 5, None) == INVALID      # N % kv heads
+    assert L.dd_tile_weight(fake, fake, 768, 256, 0, 3, None) == INVALID      # 256 rows per head
+    assert L.dd_tile_weight(fake, fake, 512, 256, 0, 2, None) == INVALID      # < 3 heads per group
+    assert L.dd_tile_weight(None, fake, 768, 256, 0, 1, None) == INVALID
     # uncached step counters: an output pointer is required; read-back needs both pointers
     assert L.dd_step_counters_alloc(None) == INVALID
     assert L.dd_step_counters_read(None, fake) == INVALID
     assert L.dd_step_counters_read(fake, None) == INVALID
-    assert L.dd_tile_weight(ctypes.c_void_p(0x1008), fake, 64, 256, 0, 0, None) == INVALID
+    assert L.dd_tile_weight(ctypes.c_void_p(0x1008), fake, 768, 256, 0, 1, None) == INVALID
 
 
 def _step_args(**kw):

@@ -17,6 +17,7 @@ import torch
 
 import dryft_amd
 from dryft_amd import synth
+from dryft_amd.step import FusedStep
 from oracle.reference import OracleEngine
 
 pytestmark = pytest.mark.gpu
@@ -31,10 +32,24 @@ def bf16_ulp(x):
 CHUNK_UNITS = [32, 16, 40, 16, 128]      # per matrix: 0 wqkv, 1 wo, 2 wgu, 3 wd, 4 lm_head
 
 
-def tiled_reference(w, matrix, G, gate_up_I=0):
+def head_grouped(w, nkv):
+    """cat(q, k, v) rows regrouped per kv head: its q heads' rows, then its k rows, then v."""
+    per = w.shape[0] // nkv
+    g = per // 128 - 2
+    nh = nkv * g
+    q, k, v = w[:nh * 128], w[nh * 128:(nh + nkv) * 128], w[(nh + nkv) * 128:]
+    return torch.cat([torch.cat([q[h * g * 128:(h + 1) * g * 128], k[h * 128:(h + 1) * 128],
+                                 v[h * 128:(h + 1) * 128]]) for h in range(nkv)])
+
+
+def tiled_reference(w, matrix, G, aux=0):
     """The step's weight layout in torch: units (rows; gate/up: features = gate row u and up row
-    I + u) split evenly over G workgroups, each workgroup's units in chunks of CHUNK_UNITS[matrix]
-    units; a chunk's weight rows (gate rows then up rows) stored k-step-major: [nk][rows][32]."""
+    I + u; QKV: rows in head-grouped order, aux = kv heads) split evenly over G workgroups, each
+    workgroup's units in chunks of CHUNK_UNITS[matrix] units; a chunk's weight rows (gate rows
+    then up rows) stored k-step-major: [nk][rows][32]."""
+    gate_up_I = aux if matrix == 2 else 0
+    if matrix == 0:
+        w = head_grouped(w, aux)
     N, K = w.shape
     nk = K // 32
     n = gate_up_I if gate_up_I else N
@@ -50,7 +65,8 @@ def tiled_reference(w, matrix, G, gate_up_I=0):
     return torch.cat(parts)
 
 
-@pytest.mark.parametrize("N,K,matrix,gu", [(768, 256, 0, 0), (6144, 2560, 0, 0), (2560, 4096, 1, 0),
+@pytest.mark.parametrize("N,K,matrix,gu", [(768, 256, 0, 1), (6144, 2560, 0, 8), (1536, 512, 0, 2),
+                                          (2560, 4096, 1, 0),
                                           (1024, 512, 1, 0), (19456, 2560, 2, 9728),
                                           (1024, 1024, 2, 512), (2560, 9728, 3, 0),
                                           (4096, 1024, 4, 0), (151936, 256, 4, 0), (100, 256, 3, 0)])
@@ -190,12 +206,12 @@ def test_fused_step_qwen3_width_b16(cuda):
     print(f"qwen3-width B=16: worst logit diff {worst:.4f}, near-tie flips {flips}")
 
 
-@pytest.mark.parametrize("B,lo,hi", [(16, 512, 8192), (1, 7000, 8000)])
+@pytest.mark.parametrize("B,lo,hi", [(16, 512, 8192), (1, 7000, 8000), (3, 512, 4096)])
 def test_fused_step_long_context(cuda, B, lo, hi):
     """configs[2]'s context range (ragged 512-8192 keys, cache capacity ~8192) through the fused
     step at Qwen3-4B widths (one layer): at B=16 every (row, kv head) is split over several
-    attention workgroups; at B=1 each of the 8 is split over ~17, past the O staging's fast path
-    of 3 contributors."""
+    attention workgroups (each XCD attending over its own kv head); at B=1 each of the 8 is split
+    over ~17 workgroups of the whole grid; B=3 is the fewest rows that take the per-XCD heads."""
     cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
     ref, eng = _engine(cfg, seed=21)
     g = torch.Generator().manual_seed(22)
@@ -249,8 +265,10 @@ def test_fused_phases_per_kernel(cuda, shape):
     pos = st.pos.cpu().clone()
     kc0, vc0 = st.kc[0].cpu(), st.vc[0].cpu()
     cpu = lambda t: t.cpu()
-    # h, attention and SiLU slots are k-step-major ([K/32][M][32]); raw q|k|v is row-major
+    # h, attention and SiLU slots are k-step-major ([K/32][M][32]); raw q|k|v is row-major and
+    # head-grouped (per kv head: its q heads, k, v)
     rows = lambda t: t.cpu().reshape(-1, B, 32).permute(1, 0, 2).reshape(B, -1)
+    qkv_rows = lambda t: FusedStep.qkv_natural(t.cpu(), eng.nh, eng.nkv)
 
     # the step's activation buffers are write-once slots: h[0] embedding, h[1] after O, h[2]
     # after down; raw q|k|v, attention output and SiLU output one slot per layer
@@ -258,13 +276,13 @@ def test_fused_phases_per_kernel(cuda, shape):
     h = rows(f.h[0])
     assert torch.equal(h.view(torch.int16), ref.embed[tok].view(torch.int16))
     qkv = ops.linear(ops.rms(h, rl.ln1), rl.wqkv)
-    _close(cpu(f.qkv[0]), qkv, "qkv projection")
+    _close(qkv_rows(f.qkv[0]), qkv, "qkv projection")
     assert torch.equal(st.kc[0].cpu(), kc0) and torch.equal(st.vc[0].cpu(), vc0)
 
     # attention: q/k RMSNorm + RoPE, K/V written at pos, attention over 0..pos
     eng.step.run(st, 2, 3)
     rkc, rvc = kc0.clone(), vc0.clone()
-    q = ops.qkv_post_rows(cpu(f.qkv[0]), rl, rkc, rvc, pos)  # [B, nh, 1, hd], writes rkc/rvc
+    q = ops.qkv_post_rows(qkv_rows(f.qkv[0]), rl, rkc, rvc, pos)  # [B, nh, 1, hd], writes rkc/rvc
     for name, c, c0, rc in (("K", st.kc[0], kc0, rkc), ("V", st.vc[0], vc0, rvc)):
         c = c.cpu()
         changed = (c != c0).any(-1).any(1)
