@@ -834,6 +834,9 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 #endif
 constexpr int ATT_OVH_MAX = DD_ATT_OVH_SMALL > DD_ATT_OVH ? DD_ATT_OVH_SMALL : DD_ATT_OVH;
 __host__ __device__ constexpr int att_ovh(int M) { return M <= 2 ? DD_ATT_OVH_SMALL : DD_ATT_OVH; }
+#ifndef DD_ATT_NOPRE
+#define DD_ATT_NOPRE 1               // waves 0 .. n-1 request no K/V block before the barrier wait
+#endif
 constexpr int ATT_QN = 32;           // query heads of all segments of one prologue round
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
@@ -988,7 +991,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     bool pre = false;
     if (sh.nseg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
-      pre = wave < ns && !(before_wait && wave == 0);   // wave 0 polls the barrier
+      pre = wave < ns && !(before_wait && wave < DD_ATT_NOPRE);   // wave 0 polls the barrier
       if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
     }
     return pre;
