@@ -237,15 +237,19 @@ WIDE = synth.qwen3_config(vocab_size=40000, hidden_size=4096, intermediate_size=
                           head_dim=128)
 
 
-@pytest.mark.parametrize("shape", ["qwen3", "small", "wide"])
+@pytest.mark.parametrize("shape", ["qwen3", "small", "wide", "kv16"])
 @torch.inference_mode()
 def test_fused_phases_per_kernel(cuda, shape):
     """Each phase of the one-launch step run on its own (phase_begin/phase_end) from the buffers
     the previous phase left, against the oracle's op on exactly those inputs (one layer, B=16
-    ragged positions; Qwen3-4B widths, the small and the wide geometry): per-kernel bf16
-    tolerance 2e-2, the embedding gather bit-exact, K/V written exactly at pos."""
+    ragged positions; Qwen3-4B widths, the small and the wide geometry, and 16 kv heads, where
+    each XCD computes and attends over two kv heads): per-kernel bf16 tolerance 2e-2, the
+    embedding gather bit-exact, K/V written exactly at pos."""
     if shape == "qwen3":
         cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192)
+    elif shape == "kv16":
+        cfg = synth.qwen3_config(num_hidden_layers=1, vocab_size=8192, num_attention_heads=32,
+                                 num_key_value_heads=16)
     elif shape == "small":
         cfg = dict(SMALL, num_hidden_layers=1)
     else:
