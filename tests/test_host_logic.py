@@ -64,3 +64,25 @@ def test_cap_rule():
 def test_engine_refuses_cpu():
     with pytest.raises(RuntimeError):
         Engine.from_state_dict(synth.qwen3_config(num_hidden_layers=1), {}, device="cpu")
+
+
+@pytest.mark.parametrize("nh,nkv", [(4, 1), (8, 2), (32, 8), (64, 8), (32, 16)])
+def test_qkv_head_grouped_order(nh, nkv):
+    """The fused step's raw q|k|v slot is head-grouped (per kv head: its nh / nkv q heads, then
+    k, then v, 128 columns each). FusedStep.qkv_natural must map it back to cat(q, k, v): applied
+    to the head-grouped order of the column indices it gives 0, 1, 2, ... and it keeps every head
+    of a group next to its own k and v (head h of group g is q head g * nh / nkv + h)."""
+    from dryft_amd.step import FusedStep
+    hd = 128
+    g = nh // nkv
+    n = (nh + 2 * nkv) * hd
+    # head-grouped order written out head by head (the layout the step's QKV phase writes)
+    order = []
+    for kv in range(nkv):
+        for h in range(g):
+            order += range((kv * g + h) * hd, (kv * g + h + 1) * hd)
+        order += range((nh + kv) * hd, (nh + kv + 1) * hd)
+        order += range((nh + nkv + kv) * hd, (nh + nkv + kv + 1) * hd)
+    grouped = torch.tensor(order).view(1, 1, n)
+    assert sorted(order) == list(range(n))
+    assert torch.equal(FusedStep.qkv_natural(grouped, nh, nkv).view(-1), torch.arange(n))
