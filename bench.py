@@ -267,14 +267,21 @@ def run_spec(torch, eng, prompts, n, W):
     return tp, ts, stats["steps"], stats["accepted_drafts"], plain == spec
 
 
-def run_prefill(torch, eng, prompts, reps=3):
+def run_prefill(torch, eng, prompts, reps=3, first=None):
     """The prompt pass of configs[4]'s ragged batch: every prompt prefilled in one packed pass
-    (GEMMs over all prompt tokens, per-prompt causal attention). Returns (ms, prompt tokens)."""
+    (GEMMs over all prompt tokens, per-prompt causal attention). Returns (ms, prompt tokens);
+    with a dict `first`, also the untimed warm-up's own time (the first pass of these lengths in
+    the process: host-side GEMM descriptors are created then) in first["ms"]."""
+    import time as _t
     B = len(prompts)
     cap = -(-max(len(p) for p in prompts) // 128) * 128
     st = eng._new_state(B, cap)
+    torch.cuda.synchronize()
+    t0 = _t.time()
     eng._prefill(prompts, st)                                 # warm-up (allocator, GEMM plans)
     torch.cuda.synchronize()
+    if first is not None:
+        first["ms"] = (_t.time() - t0) * 1e3
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -518,22 +525,30 @@ def main():
               file=sys.stderr, flush=True)
 
     # the same pass with every GEMM on F.linear (hipBLASLt's heuristic choice), then as built
-    # (each prefill GEMM on the faster of that and the library's tuned choice)
+    # (each prefill GEMM on the hipBLASLt solution the committed table names for its shape)
     os.environ["DD_TUNED_GEMM"] = "0"
     msp0, _ = run_prefill(torch, eng, prompts)
     os.environ.pop("DD_TUNED_GEMM")
-    msp, ntok = run_prefill(torch, eng, prompts)
-    picks = getattr(eng.ops, "_gemm_pick", {})
+    first = {}
+    msp, ntok = run_prefill(torch, eng, prompts, first=first)
+    from dryft_amd.hipops import gemm_solution
+    ops = eng.ops.f if hasattr(eng.ops, "f") else eng.ops
+    table = getattr(ops, "_gemm_table", {})
+    H, I = cfg["hidden_size"], cfg["intermediate_size"]
+    gshapes = {"qkv": ((eng.nh + 2 * eng.nkv) * eng.hd, H), "o": (H, eng.nh * eng.hd),
+               "gate_up": (2 * I, H), "down": (H, I)}
     extra["prefill"] = {"prompt_tokens": ntok, "ms": round(msp, 2),
                         "tok_s": round(ntok / (msp * 1e-3), 1),
+                        "first_pass_ms": round(first["ms"], 2),
                         "ms_gemms_on_f_linear": round(msp0, 2),
-                        "gemm_paths": {f"{k[0]}x{k[1]} rows={k[2]}":
-                                       "tuned hipBLASLt" if v else "F.linear"
-                                       for k, v in picks.items()},
-                        "path": "one packed pass over the 16 ragged prompts: hipBLASLt GEMMs, "
+                        "gemm_solutions": {f"{k} {n}x{kk} rows={ntok}": gemm_solution(table, n, kk, ntok)
+                                           for k, (n, kk) in gshapes.items()},
+                        "path": "one packed pass over the 16 ragged prompts: hipBLASLt GEMMs "
+                                "(the committed table's solution per shape, fixed per process), "
                                 "HIP RMSNorm / q-k norm + RoPE + K/V write / causal flash "
                                 "attention kernels"}
-    print(f"[bench] prefill {ntok} prompt tokens: {msp:.1f} ms (GEMMs on F.linear: {msp0:.1f} ms)", file=sys.stderr, flush=True)
+    print(f"[bench] prefill {ntok} prompt tokens: {msp:.1f} ms (first pass {first['ms']:.1f} ms; "
+          f"GEMMs on F.linear: {msp0:.1f} ms)", file=sys.stderr, flush=True)
 
     if not args.no_micro:
         extra["kv_layout"] = micro_kv_layout(torch, L, [n + 512 for n in lens])

@@ -13,7 +13,7 @@ import torch  # noqa: F401  (load order: see module docstring)
 
 LIB_NAME = "libdryft_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -47,6 +47,8 @@ _SIGS = {
     "dd_spec_accept": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "dd_gemm_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P, _Z, _I, _P]),
     "dd_gemm_ws_bytes": (_Z, []),
+    "dd_gemm_bf16_solutions": (_I, [_I, _I, _I, _Z, _P, _I]),
+    "dd_gemm_bf16_supported": (_I, [_I, _I, _I, _Z, _I]),
     "dd_fp8_quant": (_I, [_P, _Z, _P, _P, _P, _P]),
     "dd_fp8_quant_ws_bytes": (_Z, [_Z]),
     "dd_embed_rmsnorm": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P, _P]),
@@ -57,6 +59,8 @@ _SIGS = {
     "dd_step_counters": (_I, []),
     "dd_step_counters_alloc": (_I, [ctypes.POINTER(_P)]),
     "dd_step_counters_read": (_I, [_P, _P]),
+    "dd_step_counters_write": (_I, [_P, _P]),
+    "dd_step_counters_clear": (_I, [_P]),
     "dd_step_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "dd_tiled_bytes": (_Z, [_I, _I]),
     "dd_tile_weight": (_I, [_P, _P, _I, _I, _I, _I, _P]),

@@ -8,7 +8,7 @@
 
 namespace dd {
 
-constexpr int DD_ABI_VERSION = 14;
+constexpr int DD_ABI_VERSION = 15;
 
 inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 

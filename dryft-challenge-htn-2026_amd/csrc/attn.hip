@@ -333,16 +333,21 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_noalloc_mu;
 void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];   // device address of `scratch`, per device
 
-// Address of this device's scratch array; the first call on a device looks it up and clears the
-// counters (with a kernel on `stream`, ordered before the caller's launch).
+// Address of this device's scratch array. The first call on a device looks it up and clears the
+// counters synchronously (so no later call, on any stream, can overlap the clear); a first call
+// made while `stream` is being captured into a graph returns hipErrorStreamCaptureUnsupported
+// instead, since the clear could only be recorded, not done.
 int noalloc_scratch(hipStream_t stream, unsigned char** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
     return (int)hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   if (g_noalloc_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return (int)hipErrorInvalidValue;
+    if (cap != hipStreamCaptureStatusNone) return (int)hipErrorStreamCaptureUnsupported;
     void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(dd::scratch));
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(dd::scratch));
     if (e != hipSuccess) return (int)e;
     if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
     int* counters = (int*)((unsigned char*)ptr + dd::NOALLOC_WS_BYTES);
@@ -350,6 +355,8 @@ int noalloc_scratch(hipStream_t stream, unsigned char** out) {
                        0, stream, counters, dd::NOALLOC_COUNTERS);
     const int st = dd::launch_status();
     if (st != 0) return st;
+    e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return (int)e;
     g_noalloc_ptr[dev] = ptr;
   }
   *out = (unsigned char*)g_noalloc_ptr[dev];

@@ -1,12 +1,15 @@
-// Prefill GEMMs on hipBLASLt with the algorithm chosen by timing (host code only).
+// Prefill GEMMs on hipBLASLt with a fixed algorithm per shape (host code only).
 //
 // The prefill's projections are plain bf16 GEMMs over all prompt tokens (M in the thousands):
 // y[M,N] = x[M,K] . W[N,K]^T, fp32 accumulation, bf16 out -- the reference runs them through
 // F.linear (engine.py:131-132 via _forward, engine.py:459-503), i.e. the BLAS library's heuristic
 // choice. On MI355X hipBLASLt's first heuristic candidate is up to 25% slower than its best
 // candidate for the Qwen3-4B shapes (measured at 16,223 tokens: down 788 -> 569 us, O 382 ->
-// 247 us per layer), so the first call for a (N, K, M) times the heuristic's candidates on the
-// caller's buffers and keeps the fastest for every later call of that shape.
+// 247 us per layer). The caller names the algorithm: a hipBLASLt solution index (stable for one
+// library build), chosen offline per (N, K, M range) by timing and kept in a table the host
+// reads. The same solution on the same operands gives the same bits in every process; nothing
+// here times, allocates device memory or synchronises.
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -20,23 +23,10 @@ namespace dd {
 namespace {
 
 constexpr int MAX_DEV = 16;
-constexpr int NCAND = 16;            // heuristic candidates timed per shape
-
-struct Choice {
-  hipblasLtMatmulAlgo_t algo;
-  size_t ws;
-};
-
-// Timing runs start with cold caches: a fill of this many bytes (twice the 256 MB last-level
-// cache) evicts the operands a previous run left there, as the prefill's other kernels do
-// between its GEMMs (timed warm, an algorithm that re-reads the weights more looks faster than
-// it is in the pass).
-constexpr size_t FLUSH_BYTES = (size_t)512 << 20;
+constexpr int NCAND = 16;            // heuristic candidates listed for the tuning tool
 
 std::mutex g_mu;
 hipblasLtHandle_t g_handle[MAX_DEV] = {};
-void* g_flush[MAX_DEV] = {};
-std::map<std::tuple<int, int, int, int>, Choice> g_cache;   // (device, N, K, M)
 
 // RAII holders for a shape's descriptors (kept per shape: a prefill makes the same products
 // for every layer, and creating them per call costs host time comparable to the GEMM)
@@ -51,6 +41,16 @@ struct Desc {
     if (a) hipblasLtMatrixLayoutDestroy(a);
     if (op) hipblasLtMatmulDescDestroy(op);
   }
+};
+
+// What a (device, M, N, K, workspace) runs: the descriptors and, per requested solution index,
+// the algorithm resolved for this problem (the requested one when it supports the problem within
+// the workspace, else the heuristic's first candidate).
+struct Shape {
+  Desc d;
+  bool have_first = false;
+  hipblasLtMatmulAlgo_t first;
+  std::map<int, hipblasLtMatmulAlgo_t> algo;
 };
 
 int blas_err(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + (int)s; }
@@ -82,6 +82,82 @@ int run(hipblasLtHandle_t h, const Desc& d, const hipblasLtMatmulAlgo_t& algo, c
                                   ws, ws_bytes, stream));
 }
 
+// The handle of the current device and the (bounded) per-shape record; g_mu held.
+int shape_of(int M, int N, int K, size_t ws_bytes, hipblasLtHandle_t* h_out, Shape** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return (int)hipErrorInvalidValue;
+  if (!g_handle[dev]) {
+    const hipblasStatus_t s = hipblasLtCreate(&g_handle[dev]);
+    if (s != HIPBLAS_STATUS_SUCCESS) return blas_err(s);
+  }
+  *h_out = g_handle[dev];
+  static std::map<std::tuple<int, int, int, int, size_t>, Shape*> shapes;
+  const auto key = std::make_tuple(dev, M, N, K, ws_bytes);
+  auto it = shapes.find(key);
+  if (it == shapes.end()) {
+    if (shapes.size() >= 256) {              // bounded: drop them all (rebuilt on demand)
+      for (auto& kv : shapes) delete kv.second;
+      shapes.clear();
+    }
+    Shape* ns = new Shape;
+    const int e = make_desc(ns->d, M, N, K, ws_bytes);
+    if (e) {
+      delete ns;
+      return e;
+    }
+    it = shapes.emplace(key, ns).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+// the heuristic's candidates for the shape (up to `max`, in its order)
+int candidates(hipblasLtHandle_t h, const Desc& d, int max,
+               std::vector<hipblasLtMatmulHeuristicResult_t>& cand) {
+  cand.resize(max);
+  int n = 0;
+  const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, d.op, d.a, d.b, d.c, d.c, d.pref,
+                                                            max, cand.data(), &n);
+  if (s != HIPBLAS_STATUS_SUCCESS) return blas_err(s);
+  if (n < 1) return (int)hipErrorInvalidValue;
+  cand.resize(n);
+  return 0;
+}
+
+// The algorithm a (shape, solution) pair runs; g_mu held.
+int resolve(hipblasLtHandle_t h, Shape& sh, int solution, size_t ws_bytes,
+            const hipblasLtMatmulAlgo_t** out) {
+  auto it = sh.algo.find(solution);
+  if (it != sh.algo.end()) {
+    *out = &it->second;
+    return 0;
+  }
+  if (!sh.have_first) {
+    std::vector<hipblasLtMatmulHeuristicResult_t> cand;
+    const int e = candidates(h, sh.d, 1, cand);
+    if (e) return e;
+    sh.first = cand[0].algo;
+    sh.have_first = true;
+  }
+  hipblasLtMatmulAlgo_t pick = sh.first;
+  if (solution >= 0) {
+    std::vector<int> idx{solution};
+    std::vector<hipblasLtMatmulHeuristicResult_t> res;
+    if (hipblaslt_ext::getAlgosFromIndex(h, idx, res) == HIPBLAS_STATUS_SUCCESS && !res.empty()) {
+      const float alpha = 1.f, beta = 0.f;
+      size_t need = 0;
+      hipblasLtMatmulAlgo_t a = res[0].algo;
+      if (hipblaslt_ext::matmulIsAlgoSupported(h, sh.d.op, &alpha, sh.d.a, sh.d.b, &beta, sh.d.c,
+                                               sh.d.c, a, need) == HIPBLAS_STATUS_SUCCESS &&
+          need <= ws_bytes)
+        pick = a;
+    }
+  }
+  if (sh.algo.size() >= 64) sh.algo.clear();
+  *out = &sh.algo.emplace(solution, pick).first->second;
+  return 0;
+}
+
 }  // namespace
 }  // namespace dd
 
@@ -90,92 +166,53 @@ using namespace dd;
 DD_API size_t dd_gemm_ws_bytes(void) { return (size_t)64 << 20; }
 
 DD_API int dd_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K, void* ws,
-                        size_t ws_bytes, int tune, hipStream_t stream) {
+                        size_t ws_bytes, int solution, hipStream_t stream) {
   DD_REQUIRE(x && w && y && M >= 1 && N >= 1 && K >= 1);
   DD_REQUIRE(ws_bytes == 0 || ws != nullptr);
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return (int)hipErrorInvalidValue;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return (int)hipErrorInvalidValue;
   std::lock_guard<std::mutex> lock(g_mu);
-  if (!g_handle[dev]) {
-    const hipblasStatus_t s = hipblasLtCreate(&g_handle[dev]);
-    if (s != HIPBLAS_STATUS_SUCCESS) return blas_err(s);
-  }
-  hipblasLtHandle_t h = g_handle[dev];
-  static std::map<std::tuple<int, int, int, int, size_t>, Desc*> descs;
-  const auto dkey = std::make_tuple(dev, M, N, K, ws_bytes);
-  auto dit = descs.find(dkey);
-  if (dit == descs.end()) {
-    if (descs.size() >= 256) {               // bounded: drop them all (rebuilt on demand)
-      for (auto& kv : descs) delete kv.second;
-      descs.clear();
-    }
-    Desc* nd = new Desc;
-    const int e = make_desc(*nd, M, N, K, ws_bytes);
-    if (e) {
-      delete nd;
-      return e;
-    }
-    dit = descs.emplace(dkey, nd).first;
-  }
-  const Desc& d = *dit->second;
-  // one choice per exact shape: a choice made at another M of similar size measured up to 10%
-  // slower over a prefill pass (16,031 vs 16,223 rows)
-  const auto key = std::make_tuple(dev, N, K, M);
-  auto it = g_cache.find(key);
-  // a kept choice runs unless hipBLASLt rejects it for this M (the call validates on the host)
-  if (it != g_cache.end() && it->second.ws <= ws_bytes &&
-      run(h, d, it->second.algo, x, w, y, ws, ws_bytes, stream) == 0)
-    return 0;
-  std::vector<hipblasLtMatmulHeuristicResult_t> cand(NCAND);
+  hipblasLtHandle_t h = nullptr;
+  Shape* sh = nullptr;
+  int e = shape_of(M, N, K, ws_bytes, &h, &sh);
+  if (e) return e;
+  const hipblasLtMatmulAlgo_t* algo = nullptr;
+  e = resolve(h, *sh, solution, ws_bytes, &algo);
+  if (e) return e;
+  return run(h, sh->d, *algo, x, w, y, ws, ws_bytes, stream);
+}
+
+DD_API int dd_gemm_bf16_supported(int M, int N, int K, size_t ws_bytes, int solution) {
+  if (!(M >= 1 && N >= 1 && K >= 1 && solution >= 0)) return 0;
+  std::lock_guard<std::mutex> lock(g_mu);
+  hipblasLtHandle_t h = nullptr;
+  Shape* sh = nullptr;
+  if (shape_of(M, N, K, ws_bytes, &h, &sh)) return 0;
+  std::vector<int> idx{solution};
+  std::vector<hipblasLtMatmulHeuristicResult_t> res;
+  if (hipblaslt_ext::getAlgosFromIndex(h, idx, res) != HIPBLAS_STATUS_SUCCESS || res.empty()) return 0;
+  const float alpha = 1.f, beta = 0.f;
+  size_t need = 0;
+  hipblasLtMatmulAlgo_t a = res[0].algo;
+  return hipblaslt_ext::matmulIsAlgoSupported(h, sh->d.op, &alpha, sh->d.a, sh->d.b, &beta, sh->d.c,
+                                              sh->d.c, a, need) == HIPBLAS_STATUS_SUCCESS &&
+                 need <= ws_bytes
+             ? 1
+             : 0;
+}
+
+DD_API int dd_gemm_bf16_solutions(int M, int N, int K, size_t ws_bytes, int* out, int max) {
+  if (!(M >= 1 && N >= 1 && K >= 1 && out && max >= 1)) return -1;
+  std::lock_guard<std::mutex> lock(g_mu);
+  hipblasLtHandle_t h = nullptr;
+  Shape* sh = nullptr;
+  int e = shape_of(M, N, K, ws_bytes, &h, &sh);
+  if (e) return -1;
+  std::vector<hipblasLtMatmulHeuristicResult_t> cand;
+  e = candidates(h, sh->d, max < NCAND ? max : NCAND, cand);
+  if (e) return -1;
   int n = 0;
-  hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, d.op, d.a, d.b, d.c, d.c, d.pref, NCAND,
-                                                      cand.data(), &n);
-  if (s != HIPBLAS_STATUS_SUCCESS) return blas_err(s);
-  if (n < 1) return (int)hipErrorInvalidValue;
-  // no timing under graph capture or when asked not to: the heuristic's first candidate
-  if (!tune || cap != hipStreamCaptureStatusNone) return run(h, d, cand[0].algo, x, w, y, ws, ws_bytes, stream);
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-    if (e0) (void)hipEventDestroy(e0);
-    return (int)hipErrorOutOfMemory;
+  for (auto& c : cand) {
+    if (c.state != HIPBLAS_STATUS_SUCCESS || c.workspaceSize > ws_bytes) continue;
+    out[n++] = hipblaslt_ext::getIndexFromAlgo(c.algo);
   }
-  if (!g_flush[dev] && hipMalloc(&g_flush[dev], FLUSH_BYTES) != hipSuccess) {
-    g_flush[dev] = nullptr;
-    (void)hipGetLastError();
-  }
-  // each usable candidate: one warm-up, then the least of 3 single runs, each after a cache
-  // flush (the least is the one least disturbed by other work on the device)
-  int best = -1;
-  float best_ms = 0.f;
-  for (int i = 0; i < n; ++i) {
-    if (cand[i].state != HIPBLAS_STATUS_SUCCESS || cand[i].workspaceSize > ws_bytes) continue;
-    if (run(h, d, cand[i].algo, x, w, y, ws, ws_bytes, stream)) continue;   // warm-up
-    bool ok = true;
-    float ms = 0.f;
-    for (int trial = 0; trial < 3 && ok; ++trial) {
-      if (g_flush[dev]) (void)hipMemsetAsync(g_flush[dev], trial, FLUSH_BYTES, stream);
-      (void)hipEventRecord(e0, stream);
-      ok = run(h, d, cand[i].algo, x, w, y, ws, ws_bytes, stream) == 0;
-      (void)hipEventRecord(e1, stream);
-      float t = 0.f;
-      if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&t, e0, e1) != hipSuccess) {
-        ok = false;
-        break;
-      }
-      ms = trial == 0 ? t : (t < ms ? t : ms);
-    }
-    if (!ok) continue;
-    if (best < 0 || ms < best_ms) {
-      best = i;
-      best_ms = ms;
-    }
-  }
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (best < 0) best = 0;
-  g_cache[key] = Choice{cand[best].algo, cand[best].workspaceSize};
-  // the result the caller asked for (the timing runs wrote the same product)
-  return run(h, d, cand[best].algo, x, w, y, ws, ws_bytes, stream);
+  return n;
 }

@@ -1,7 +1,8 @@
 // Tensorwise fp8 (OCP e4m3, the gfx950 format) quantisation of prefill GEMM activations
 // (fused.py:130-149: quant_fp8_tensorwise), two launches:
 //   amax_kernel   per-workgroup max |x| over a grid-stride range -> partials[gridDim.x]
-//   quant_kernel  every workgroup folds the partials (amax, clamped to >= 1e-6), block 0 writes
+//   quant_kernel  every workgroup folds the partials (amax, clamped to >= 1e-6; a NaN in x
+//                 makes it NaN, as torch's amax and clamp do), block 0 writes
 //                 scale = amax / 448 (the GEMM's dequantisation factor); q = e4m3(x * (448 / amax))
 // x is bf16, read as 16-byte vectors (8 elements); the conversion rounds to nearest even and
 // turns magnitudes past 464 (half-way to the first value past the largest finite 448, which
@@ -14,6 +15,15 @@ namespace f8 {
 
 constexpr int THREADS = 256;
 constexpr int MAXBLK = 1024;
+
+// max that keeps a NaN (torch's amax and clamp propagate it: a NaN anywhere in x makes the scale,
+// and so every quantised value, NaN)
+__device__ __forceinline__ float nanmax(float a, float b) { return (a != a || a > b) ? a : b; }
+__device__ __forceinline__ float wave_nanmax(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nanmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
 
 // fp32 -> e4m3fn bits (1 sign, 4 exponent bits with bias 7, 3 mantissa bits; 0x7f/0xff NaN)
 __device__ __forceinline__ unsigned e4m3(float x) {
@@ -39,14 +49,14 @@ amax_kernel(const u32x4* __restrict__ x, size_t n8, float* __restrict__ partials
     const u32x4 v = x[i];
     const unsigned w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(lo_bf(w[j])), fabsf(hi_bf(w[j]))));
+    for (int j = 0; j < 4; ++j) m = nanmax(m, nanmax(fabsf(lo_bf(w[j])), fabsf(hi_bf(w[j]))));
   }
-  m = wave_max(m);
+  m = wave_nanmax(m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) {
     float t = red[0];
-    for (int k = 1; k < THREADS / 64; ++k) t = fmaxf(t, red[k]);
+    for (int k = 1; k < THREADS / 64; ++k) t = nanmax(t, red[k]);
     partials[blockIdx.x] = t;
   }
 }
@@ -56,13 +66,13 @@ quant_kernel(const u32x4* __restrict__ x, size_t n8, const float* __restrict__ p
              uint2* __restrict__ out, float* __restrict__ scale) {
   __shared__ float red[THREADS / 64];
   float m = 0.f;
-  for (int i = threadIdx.x; i < np; i += THREADS) m = fmaxf(m, partials[i]);
-  m = wave_max(m);
+  for (int i = threadIdx.x; i < np; i += THREADS) m = nanmax(m, partials[i]);
+  m = wave_nanmax(m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   float amax = red[0];
-  for (int k = 1; k < THREADS / 64; ++k) amax = fmaxf(amax, red[k]);
-  amax = fmaxf(amax, 1e-6f);
+  for (int k = 1; k < THREADS / 64; ++k) amax = nanmax(amax, red[k]);
+  amax = nanmax(amax, 1e-6f);
   const float inv = 448.0f / amax;
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = amax / 448.0f;
   for (size_t i = blockIdx.x * (size_t)THREADS + threadIdx.x; i < n8; i += (size_t)gridDim.x * THREADS) {

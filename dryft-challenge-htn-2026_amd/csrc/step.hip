@@ -2294,6 +2294,27 @@ DD_API int dd_step_counters_read(const void* counters, int* host) {
   return (int)hipMemcpy(host, counters, C_TOTAL * sizeof(int), hipMemcpyDeviceToHost);
 }
 
+// Diagnostics and tests: overwrite the dd_step_counters() ints at `counters` from host memory
+// (waits for the device first; synchronous).
+DD_API int dd_step_counters_write(void* counters, const int* host) {
+  DD_REQUIRE(counters != nullptr && host != nullptr);
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(counters, host, C_TOTAL * sizeof(int), hipMemcpyHostToDevice);
+  return (int)e;
+}
+
+// Zero every counter after a launch that timed out at a grid barrier (error flag 4): its
+// workgroups stopped waiting, so the hand-off counters that their last arrivers reset (attention
+// combines, split down pairs, argmax) may be left nonzero. Waits for the device first; not for
+// use under graph capture.
+DD_API int dd_step_counters_clear(void* counters) {
+  DD_REQUIRE(counters != nullptr);
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemset(counters, 0, C_TOTAL * sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  return (int)e;
+}
+
 DD_API size_t dd_step_ws_bytes(int L, int NH, int NKV, int W) {
   int G = 0;
   if (L < 1 || NKV < 1 || NH < NKV || W < 1 || W > MAXW || step_grid(&G) != 0) return 0;

@@ -3,8 +3,9 @@ pipelined host loop, decode kernels from libdryft_decode.so.
 
 Mirrors the reference ``Engine`` API (engine/engine.py:247-279, 683-732):
 ``Engine(model_path)`` loads an HF-named safetensors checkpoint, ``generate(input_ids, n)``
-yields one ``list[int]`` (one token per sequence) per step. Plain greedy decoding only (the
-reference's speculative and fp8 paths are not part of this build).
+yields one ``list[int]`` (one token per sequence) per step. Greedy decoding; the reference's
+in-graph speculation (exact acceptance only, ``speculate.py``) and fp8 prefill GEMMs are opt-in
+with its own switches (``ENGINE_SPEC=1``, ``ENGINE_FP8=1``).
 
 Differences by design (MI355X-first):
   * decode positions are per row (``st.pos`` is ``[B]``), so a ragged batch decodes in ONE state
@@ -465,7 +466,7 @@ class Engine:
         elif len(set(lens)) == 1:
             ids = torch.tensor(input_ids, dtype=torch.long, device=self.dev)
             B, S = ids.shape
-            st.tok.copy_(self._forward(st, ids.reshape(-1), S, None).argmax(-1))
+            st.tok[:B].copy_(self._forward(st, ids.reshape(-1), S, None).argmax(-1))
         else:
             dbg = self._dbg
             rows = []
@@ -504,6 +505,8 @@ class Engine:
             self._grow_rope(cap)
         st = self._state(B, cap, graph=n > 1)
         self._host_bufs(st, n)
+        if st.fused is not None:
+            self.recover(int(st.err.item()))   # a barrier timeout left by an earlier call
         self._clear_errors(st)
         self._prefill(input_ids, st)
         host, ev = st.host, st.events
@@ -527,12 +530,20 @@ class Engine:
         if err is not None:
             err.zero_()
 
-    @staticmethod
-    def _checked(row, t):
+    def recover(self, flags):
+        """After a step that flagged a grid-barrier timeout (flag 4) the one-launch step's
+        counters may be left nonzero (its workgroups stopped waiting, so hand-off counters that
+        their last arrivers reset can keep a count): zero them before the next launch.
+        Synchronises the device when it acts."""
+        if flags & 4 and self.step is not None:
+            self.step.reset_counters()
+
+    def _checked(self, row, t):
         """Tokens of one step from the host ring, after its error word (the ring's last column):
         a step that flagged an error raises instead of yielding tokens computed from it."""
         flags = int(row[-1]) & 0xffffffff
         if flags:
+            self.recover(flags)
             raise RuntimeError(f"decode step {t} reported error flags {flags:#x} ({describe_flags(flags)})")
         return row[:-1].tolist()
 
@@ -557,4 +568,5 @@ class Engine:
         flags = int(ops.err.item()) if hasattr(ops, "err") else 0
         for st in self.states.values():
             flags |= int(st.err.item())
+        self.recover(flags)
         return flags

@@ -14,6 +14,8 @@ Every decode-step method calls the C ABI on torch's current stream; outputs and 
 allocated with ``torch.empty`` (so they come from the graph pool under capture). A nonzero
 status raises ``RuntimeError``.
 """
+import json
+import math
 import os
 
 import torch
@@ -29,16 +31,34 @@ def _ptr(t):
     return t.data_ptr() if t is not None else None
 
 
-def _time_cold_ms(f, flush):
-    """Time of one f() on the current stream after a fill of `flush` (larger than the last-level
-    cache), so f starts with cold caches as it does between the prefill's other kernels."""
-    flush.fill_(0)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    f()
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1)
+# hipBLASLt solution per prefill GEMM shape and row range (tune_gemm.py writes it on the GPU)
+GEMM_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_solutions.json")
+
+
+def load_gemm_table(path=GEMM_TABLE):
+    """{(N, K): [(M, solution), ...] sorted by M} from the committed table, or {} when it is
+    absent (every shape then runs hipBLASLt's first heuristic candidate)."""
+    try:
+        with open(path) as f:
+            doc = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    out = {}
+    for key, rows in doc.get("shapes", {}).items():
+        n, k = (int(v) for v in key.split("x"))
+        out[(n, k)] = sorted((int(m), int(sol)) for m, sol in rows)
+    return out
+
+
+def gemm_solution(table, N, K, M):
+    """The table's solution for an (N, K) product of M rows: the entry whose row count is
+    nearest to M on a log scale (the smaller on a tie), or -1 (heuristic first) for shapes the
+    table lacks."""
+    rows = table.get((N, K))
+    if not rows:
+        return -1
+    lm = math.log(M)
+    return min(rows, key=lambda r: abs(math.log(r[0]) - lm))[1]
 
 
 def _stream(dev):
@@ -90,7 +110,7 @@ class HipOps:
         self.L = lib()  # raises when the library is missing: no silent fallback
         self._counters = None
         self._gemm_ws = None
-        self._gemm_pick = {}
+        self._gemm_table = load_gemm_table()
         self._starts = {}
         self.err = torch.zeros(1, dtype=torch.int32, device=e.dev)
 
@@ -109,45 +129,30 @@ class HipOps:
                 and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
 
     def _gemm_ok(self, x, w):
-        """Prefill-sized bf16 products may go to the library's tuned hipBLASLt GEMM
-        (dd_gemm_bf16); DD_TUNED_GEMM=0 keeps them on F.linear (the library's heuristic choice)."""
+        """Prefill-sized bf16 products go to the library's hipBLASLt GEMM (dd_gemm_bf16) with the
+        solution the committed table names for the shape; DD_TUNED_GEMM=0 keeps them on F.linear
+        (diagnostics)."""
         return (x.dim() == 2 and x.shape[0] >= GEMM_MIN_M and _bf16_ok(x, w)
                 and os.environ.get("DD_TUNED_GEMM", "1") != "0")
 
-    def _gemm_lib(self, x, w):
+    def _gemm_lib(self, x, w, solution=None):
         M, K = x.shape
         N = w.shape[0]
+        if solution is None:
+            solution = gemm_solution(self._gemm_table, N, K, M)
         ws = self._gemm_ws
         if ws is None or ws.device != x.device:
             ws = self._gemm_ws = torch.empty(self.L.dd_gemm_ws_bytes(), dtype=torch.uint8,
                                              device=x.device)
         y = torch.empty((M, N), dtype=x.dtype, device=x.device)
-        check(self.L.dd_gemm_bf16(_ptr(x), _ptr(w), _ptr(y), M, N, K, _ptr(ws), ws.numel(), 1,
-                                  _stream(x.device)), "dd_gemm_bf16")
+        check(self.L.dd_gemm_bf16(_ptr(x), _ptr(w), _ptr(y), M, N, K, _ptr(ws), ws.numel(),
+                                  solution, _stream(x.device)), "dd_gemm_bf16")
         return y
 
     def _gemm(self, x, w):
-        """y = x . w^T through whichever of the library's tuned GEMM and F.linear was faster for
-        this (N, K, M) when first met: the first call (outside graph capture) tunes the library's
-        choice, then times both on these operands from cold caches; the pick is kept for the
-        process, so every later product of the shape takes the same path (same bits)."""
-        x, w = x.contiguous(), w.contiguous()
-        M, K = x.shape
-        key = (w.shape[0], K, M, x.device)
-        use_lib = self._gemm_pick.get(key)
-        if use_lib is None:
-            if torch.cuda.is_current_stream_capturing():
-                return F.linear(x, w)
-            self._gemm_lib(x, w)                              # tunes the library's choice
-            F.linear(x, w)
-            flush = torch.empty(512 << 20, dtype=torch.uint8, device=x.device)
-            t_lib = t_ref = float("inf")
-            for _ in range(3):                                # interleaved; the least of each
-                t_lib = min(t_lib, _time_cold_ms(lambda: self._gemm_lib(x, w), flush))
-                t_ref = min(t_ref, _time_cold_ms(lambda: F.linear(x, w), flush))
-            del flush
-            use_lib = self._gemm_pick[key] = t_lib < t_ref
-        return self._gemm_lib(x, w) if use_lib else F.linear(x, w)
+        """y = x . w^T on hipBLASLt with the table's solution for (N, K, M): a fixed choice per
+        shape, so every process computes the same bits for the same operands."""
+        return self._gemm_lib(x.contiguous(), w.contiguous())
 
     # ---------------------------------------------------------------- norms
     def rms(self, h, w):
@@ -262,24 +267,19 @@ class HipOps:
     def fp8_linear(self, x, w8, w_scale, w):
         """engine.py:451-457: y = x @ w^T with x quantised tensorwise to fp8 e4m3 by the HIP
         kernel and w8 / w_scale the weight's tensorwise fp8 copy, on hipBLASLt (torch._scaled_mm)
-        with bf16 output. Fewer than 16 rows take the bf16 ``linear``; a row count that is not a
-        multiple of 16 (the GEMM's granule) is padded with zero rows, where the reference falls
-        back to bf16 (the scale is taken over the real rows only)."""
+        with bf16 output. As in the reference's _fp8_lin, a row count that is not a multiple of
+        16 (the fp8 GEMM's granule) takes the bf16 ``linear`` instead."""
         x = x.contiguous()
         M, K = x.shape
-        if M < 16 or K % 16 != 0 or not _bf16_ok(x):
+        if M % 16 != 0 or K % 16 != 0 or not _bf16_ok(x):
             return self.linear(x, w)
-        M16 = -(-M // 16) * 16
-        xq = torch.empty((M16, K), dtype=torch.float8_e4m3fn, device=x.device)
-        if M16 != M:
-            xq[M:].view(torch.uint8).zero_()
+        xq = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
         xs = torch.empty((1, 1), dtype=torch.float32, device=x.device)
         ws = torch.empty(self.L.dd_fp8_quant_ws_bytes(M * K) // 4, dtype=torch.float32,
                          device=x.device)
         check(self.L.dd_fp8_quant(_ptr(x), M * K, _ptr(xq), _ptr(xs), _ptr(ws), _stream(x.device)),
               "dd_fp8_quant")
-        y = torch._scaled_mm(xq, w8.t(), scale_a=xs, scale_b=w_scale, out_dtype=torch.bfloat16)
-        return y[:M] if M16 != M else y
+        return torch._scaled_mm(xq, w8.t(), scale_a=xs, scale_b=w_scale, out_dtype=torch.bfloat16)
 
     # ---------------------------------------------------------------- prefill
     def _seq_start(self, B, S, dev):

@@ -121,6 +121,7 @@ class Speculator:
         if cap > e.cos.shape[0]:
             e._grow_rope(cap)
         st = self.state(B, cap, graph)
+        e.recover(int(st.err.item()))              # a barrier timeout left by an earlier call
         e._clear_errors(st)
         e._prefill(input_ids, st)                  # first tokens in st.tok[:B]
         dev = e.dev
@@ -174,6 +175,7 @@ class Speculator:
             row = host[t]
             flags = int(row[-1]) & 0xffffffff
             if flags:
+                self.e.recover(flags)
                 raise RuntimeError(f"speculative step {t} reported error flags {flags:#x}")
             o = row[:B * W].view(B, W).tolist()
             a = row[B * W:B * W + B].tolist()

@@ -64,7 +64,8 @@ class FusedStep:
 
     def _counters(self):
         """The step's barrier and hand-off counters, one zeroed buffer shared by every state of
-        this engine: each launch leaves them zero, and the engine runs one launch at a time
+        this engine: each launch leaves them zero (a launch that timed out at a barrier may not;
+        the engine then calls reset_counters), and the engine runs one launch at a time
         (launches that overlap in time must not share them). They live in uncached device
         memory allocated by the library (never freed), unless DD_UC_COUNTERS=0 asks for an
         ordinary zeroed tensor."""
@@ -78,6 +79,13 @@ class FusedStep:
                                           device=self.e.dev)
                 self._ctr = self._ctr_t.data_ptr()
         return self._ctr
+
+    def reset_counters(self):
+        """Zero the step's counters (synchronous): needed after a launch that set error flag 4
+        (a grid barrier timed out), whose workgroups stopped waiting and may have left hand-off
+        counters nonzero; every state of this engine shares them."""
+        if self._ctr is not None:
+            check(self.L.dd_step_counters_clear(self._ctr), "dd_step_counters_clear")
 
     def _tile(self, w, matrix, aux=0):
         N, K = w.shape
@@ -162,6 +170,12 @@ class FusedStep:
         host = (ctypes.c_int * n)()
         check(self.L.dd_step_counters_read(st.fused.counters_ptr, host), "dd_step_counters_read")
         return list(host)
+
+    def write_counters(self, st, values):
+        """Overwrite a state's step counters from a host list (tests and diagnostics)."""
+        n = self.L.dd_step_counters()
+        host = (ctypes.c_int * n)(*values)
+        check(self.L.dd_step_counters_write(st.fused.counters_ptr, host), "dd_step_counters_write")
 
 
 class _State:

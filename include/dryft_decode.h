@@ -10,8 +10,13 @@
  *  - All tensors are device pointers to contiguous row-major memory on the current HIP device.
  *    bf16 tensors are passed as ``const void*`` / ``void*`` (16-bit patterns); fp32 workspaces
  *    as ``void*``; positions and token ids as int64 (torch.long).
- *  - Every call is asynchronous on ``stream`` and capture-safe: no allocation, no host sync,
- *    positions are read from device memory.
+ *  - The kernel entry points (everything that takes a ``stream``) are asynchronous on it and
+ *    capture-safe: no device allocation, no host sync, positions are read from device memory.
+ *    dd_gemm_bf16 keeps that contract too; its first call of a shape creates hipBLASLt
+ *    descriptors on the host. The exceptions are set-up and diagnostics calls, marked where
+ *    they are declared: dd_step_counters_alloc (allocates), dd_step_counters_read / _write /
+ *    _clear (synchronous) and dd_attn_decode_noalloc's first call on a device (a synchronous
+ *    clear of its static counters).
  *  - Return value: 0 on success; hipErrorInvalidValue (1) when an argument fails validation
  *    (nothing is launched then); otherwise the hipError_t reported by the launch. Nothing throws
  *    across the ABI.
@@ -113,8 +118,10 @@ size_t dd_attn_ws_bytes(int B, int W, int NH, int NKV, int HD, int cap, int chun
  * array of 24 MiB + 16 KiB per GPU, held until the process ends; the key chunk is always
  * dd_attn_chunk(B, NKV, cap). Shapes whose dd_attn_ws_bytes exceeds 24 MiB, or with
  * B * NKV > 4096, return hipErrorOutOfMemory (2) and launch nothing. The first call on a device
- * looks the array up and clears its counters (a kernel on `stream`); every call leaves them
- * zero. All calls on one GPU share the array: calls that overlap in time on one GPU race. The
+ * looks the array up and clears its counters (a fill kernel on `stream`, then a wait for the
+ * stream), so it must not be made under graph capture: there it returns
+ * hipErrorStreamCaptureUnsupported and launches nothing; make one call outside capture first.
+ * Every call leaves the counters zero. All calls on one GPU share the array: calls that overlap in time on one GPU race. The
  * output equals dd_attn_decode's with the same chunk, bit for bit. */
 int dd_attn_decode_noalloc(const void* q, const void* kc, const void* vc, const int64_t* pos,
                            int pos_stride, void* out, int B, int W, int NH, int NKV, int HD,
@@ -147,15 +154,23 @@ int dd_attn_prefill(const void* q, const void* kc, const void* vc, const int* se
                     hipStream_t stream);
 
 /* Prefill GEMM: y[M,N] = x[M,K] . W[N,K]^T, bf16 in and out, fp32 accumulation, on hipBLASLt.
- * With tune != 0 the first call for a (N, K, M) outside graph capture times the library's
- * heuristic candidates on the caller's buffers, each after a cache flush (this synchronises the
- * stream and allocates inside the library) and keeps the fastest for later calls of that shape;
- * under graph capture, or with tune == 0 and no kept choice, the heuristic's first candidate
- * runs, without a host sync. ws: at least dd_gemm_ws_bytes() bytes of device memory (hipBLASLt workspace).
+ * solution >= 0 names the hipBLASLt solution to run (an index from dd_gemm_bf16_solutions,
+ * stable for one hipBLASLt build); when it does not support this problem within ws_bytes, or
+ * solution < 0, the heuristic's first candidate runs. The choice depends only on the arguments,
+ * so the same operands give the same bits in every process. No timing, no device allocation, no
+ * host sync (the first call of a shape creates hipBLASLt descriptors on the host); safe under
+ * graph capture. ws: at least dd_gemm_ws_bytes() bytes of device memory (hipBLASLt workspace).
  * Replaces the prefill's F.linear of _TorchOps.linear (engine.py:131-132) in Engine._forward
  * over all prompt tokens (engine.py:459-503). */
 int dd_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K, void* ws,
-                 size_t ws_bytes, int tune, hipStream_t stream);
+                 size_t ws_bytes, int solution, hipStream_t stream);
+/* The solution indices of hipBLASLt's heuristic candidates for the product (up to max of them,
+ * in the heuristic's order, those that fit ws_bytes), written to out; returns their number, or
+ * -1. For the offline tuning tool that builds the host's solution table (tune_gemm.py). */
+int dd_gemm_bf16_solutions(int M, int N, int K, size_t ws_bytes, int* out, int max);
+/* 1 when hipBLASLt solution `solution` supports the product within ws_bytes (dd_gemm_bf16 then
+ * runs it), else 0. For the tuning tool. */
+int dd_gemm_bf16_supported(int M, int N, int K, size_t ws_bytes, int solution);
 size_t dd_gemm_ws_bytes(void);
 
 /* Tensorwise fp8 quantisation of a prefill GEMM input: x [n] bf16 (n a multiple of 8, x 16-byte
@@ -216,6 +231,14 @@ int dd_step_counters(void);
 int dd_step_counters_alloc(void** out);
 /* Diagnostics: synchronous copy of the dd_step_counters() ints at `counters` to `host`. */
 int dd_step_counters_read(const void* counters, int* host);
+/* Diagnostics and tests: synchronous copy of dd_step_counters() ints from `host` to
+ * `counters` (waits for the device first). No counterpart in the reference. */
+int dd_step_counters_write(void* counters, const int* host);
+/* Zeroes every counter (waits for the device first; synchronous; not under graph capture).
+ * Needed after a launch that set error flag 4 (a grid barrier timed out): its workgroups stopped
+ * waiting, so hand-off counters their last arrivers would have reset may be left nonzero. No
+ * counterpart in the reference: recovery of the persistent step's caller-owned counters. */
+int dd_step_counters_clear(void* counters);
 size_t dd_step_ws_bytes(int L, int NH, int NKV, int W);
 size_t dd_tiled_bytes(int N, int K);
 int dd_tile_weight(const void* src, void* dst, int N, int K, int matrix, int aux,

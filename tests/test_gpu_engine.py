@@ -116,6 +116,31 @@ def test_generate_raises_on_error_flag(tiny):
 
 
 @torch.inference_mode()
+def test_counters_recovered_after_barrier_timeout(tiny):
+    """Recovery from a grid-barrier timeout of the one-launch step (error flag 4), forced from
+    the host so no kernel waits: the counters are poisoned the way a timed-out launch can leave
+    them (attention-combine, argmax and split-down counts nonzero) and the state's error word
+    carries flag 4; the next generate() must zero the counters first and produce the same
+    tokens as a clean run, leaving every counter zero."""
+    _, eng = tiny
+    if eng.step is None:
+        pytest.skip("per-op path: no one-launch step counters")
+    ids = torch.randint(0, 1024, (3, 40), generator=torch.Generator().manual_seed(17)).tolist()
+    want = list(eng.generate(ids, 6))
+    st = eng.states[(3, 128, 1, True)]
+    n = eng.step.L.dd_step_counters()
+    poison = [0] * n
+    for i in range(1024, n):                 # hand-off counters (not the barrier counters)
+        poison[i] = 1 + i % 3
+    eng.step.write_counters(st, poison)
+    st.err.fill_(4)                          # what the timed-out launch reported
+    got = list(eng.generate(ids, 6))
+    assert got == want
+    assert eng.step.counters(st) == [0] * n
+    assert eng.error_flags() == 0
+
+
+@torch.inference_mode()
 def test_graph_replay_equals_eager(tiny):
     """The captured step must reproduce eager steps bit for bit (replayed several times, with
     eager work and syncs in between)."""

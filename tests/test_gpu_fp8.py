@@ -4,6 +4,7 @@ ties included), the fp8 GEMM against a float64 product of the dequantised operan
 prefill through the engine with fp8 QKV and gate/up projections against the bf16 oracle (the
 reference's 2.0-logit gate: the path is not bf16-exact by design, engine.py:97-104).
 """
+import math
 import os
 
 import pytest
@@ -69,6 +70,18 @@ def test_quant_rounding_edges(cuda):
     assert q.cpu().view(torch.uint8).tolist() == wq.view(torch.uint8).tolist()
 
 
+def test_quant_nan_propagates(cuda):
+    """A NaN anywhere in x makes the scale NaN and every quantised value NaN, as torch's amax and
+    clamp (the reference's quantisation, fused.py:130-149) propagate it."""
+    x = torch.randn(4096, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    x[1234] = float("nan")
+    q, sc = _quant(x.cuda())
+    assert math.isnan(float(sc))
+    assert torch.isnan(q.cpu().float()).all()
+    wq, wsc = _torch_quant(x)
+    assert math.isnan(float(wsc)) and torch.isnan(wq.float()).all()
+
+
 def test_fp8_linear_matches_dequantised_product(cuda):
     from dryft_amd.hipops import HipOps
     import types
@@ -86,12 +99,14 @@ def test_fp8_linear_matches_dequantised_product(cuda):
     d = (y.double() - ref).abs().max().item()
     scale = ref.abs().max().item()
     assert d <= 1e-2 * scale, (d, scale)
-    # fewer than 16 rows take the bf16 path; other row counts are padded to the 16-row granule
+    # a row count that is not a multiple of 16 takes the bf16 path, as the reference's _fp8_lin
+    # does (engine.py:451-454); 48 rows (a multiple) stay on fp8
     assert torch.equal(ops.fp8_linear(x[:5], w8, s, w), ops.linear(x[:5], w))
-    y37 = ops.fp8_linear(x[:37], w8, s, w)
-    xq37, xs37 = _quant(x[:37].contiguous())
-    ref37 = (xq37.double() * float(xs37)) @ (w8.double() * float(s)).T
-    assert y37.shape == (37, N) and (y37.double() - ref37).abs().max().item() <= 1e-2 * scale
+    assert torch.equal(ops.fp8_linear(x[:37], w8, s, w), ops.linear(x[:37], w))
+    y48 = ops.fp8_linear(x[:48], w8, s, w)
+    xq48, xs48 = _quant(x[:48].contiguous())
+    ref48 = (xq48.double() * float(xs48)) @ (w8.double() * float(s)).T
+    assert y48.shape == (48, N) and (y48.double() - ref48).abs().max().item() <= 1e-2 * scale
     bf = torch.nn.functional.linear(x, w)
     print(f"fp8 GEMM: max|y - dequantised fp64| {d:.3g} (scale {scale:.3g}); "
           f"max|y - bf16 linear| {(y - bf).abs().max().item():.3g}")
@@ -112,7 +127,7 @@ def test_engine_fp8_prefill_gate(cuda, monkeypatch):
     eng = Engine.from_state_dict(SMALL, {k: v.cuda() for k, v in w.items()})
     assert eng.fp8 and hasattr(eng.layers[0], "wqkv8")
     g = torch.Generator().manual_seed(9)
-    lens = [16, 37, 44]                                   # 97 packed rows: padded to 112
+    lens = [16, 37, 43]                                   # 96 packed rows: the fp8 GEMMs
     prompts = [torch.randint(0, 1024, (n,), generator=g).tolist() for n in lens]
     st = eng._new_state(len(lens), 128)
     eng._dbg = []

@@ -218,6 +218,41 @@ def test_configs4_packed_prefill(full):
           f"logit diff vs per-prompt torch {worst:.4f}")
 
 
+@pytest.mark.timeout(600)
+@torch.inference_mode()
+def test_configs4_prefill_deterministic(full):
+    """The packed prefill of configs[4]'s 16 prompts gives the same bits from two fresh HipOps
+    instances of this process and from a fresh process (its own engine, weights rebuilt from the
+    same seed): every prefill GEMM runs the hipBLASLt solution the committed table names for its
+    shape, with no timing at run time, so nothing depends on the process."""
+    import os
+    import subprocess
+    import sys
+    from dryft_amd.hipops import HipOps
+    from prefill_bits import prefill_digest
+    cfg, _, eng = full
+    prompts = configs4_prompts(cfg["vocab_size"])
+    saved = eng.ops
+    digests = []
+    try:
+        for _ in range(2):
+            eng.ops = HipOps(eng)
+            digests.append(prefill_digest(eng, prompts))
+    finally:
+        eng.ops = saved
+    assert digests[0] == digests[1]
+    here = os.path.dirname(os.path.abspath(__file__))
+    out = subprocess.run([sys.executable, os.path.join(here, "prefill_bits.py")],
+                         capture_output=True, text=True, timeout=540)
+    line = [x for x in out.stdout.splitlines() if x.startswith("PREFILL ")]
+    assert out.returncode == 0 and line, out.stderr[-2000:]
+    digest, toks = line[0].split(" ", 2)[1:]
+    assert digest == digests[0][0], "another process computed different prefill logits"
+    assert [int(t) for t in toks.split()] == digests[0][1]
+    print(f"configs[4] packed prefill: logits sha256 {digest[:16]} identical across two HipOps "
+          f"instances and a fresh process")
+
+
 @torch.inference_mode()
 def test_configs4_fp8_prefill_gate(full):
     """Opt-in fp8 prefill GEMMs (QKV and gate/up, tensorwise e4m3, B <= 8) at full size: the

@@ -223,11 +223,13 @@ def test_linear_dtype_and_layout_fallback(small):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 512, 256), (777, 2560, 1024), (2049, 1536, 512)])
-def test_tuned_gemm_matches_fp32(small, M, N, K):
-    """Prefill-sized products (M >= GEMM_MIN_M) through dd_gemm_bf16: the tuned call, a second
-    call of the same shape (the kept choice) and HipOps.linear's pick all within the bf16 bar of
-    an fp32 product, the kept choice bit-identical to the tuned call, tune=0 (heuristic first
-    candidate) likewise within the bar."""
+def test_gemm_solutions_match_fp32(small, M, N, K):
+    """Prefill-sized products (M >= GEMM_MIN_M) through dd_gemm_bf16: the heuristic's first
+    candidate (solution -1) and every candidate dd_gemm_bf16_solutions lists, each within the
+    bf16 bar of an fp32 product and each the same bits when called again; a solution index that
+    names no hipBLASLt solution runs the heuristic's first candidate (same bits as -1);
+    HipOps.linear (the committed table's pick) within the bar."""
+    import ctypes
     from dryft_amd.hipops import GEMM_MIN_M
     _, hip, _ = small
     g = torch.Generator().manual_seed(M + N + K)
@@ -236,20 +238,32 @@ def test_tuned_gemm_matches_fp32(small, M, N, K):
     ref = x.float() @ w.float().T
     xc, wc = x.cuda(), w.cuda()
     assert M >= GEMM_MIN_M
-    y1 = hip._gemm_lib(xc, wc)
-    y2 = hip._gemm_lib(xc, wc)
-    assert torch.equal(y1, y2)
-    close(y1, ref)
-    close(hip.linear(xc, wc), ref)
     ws = torch.empty(hip.L.dd_gemm_ws_bytes(), dtype=torch.uint8, device="cuda")
-    y0 = torch.empty(M, N, dtype=BF, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
-    assert hip.L.dd_gemm_bf16(xc.data_ptr(), wc.data_ptr(), y0.data_ptr(), M, N, K, ws.data_ptr(),
-                              ws.numel(), 0, stream) == 0
-    close(y0, ref)
+
+    def run(sol):
+        y = torch.empty(M, N, dtype=BF, device="cuda")
+        assert hip.L.dd_gemm_bf16(xc.data_ptr(), wc.data_ptr(), y.data_ptr(), M, N, K,
+                                  ws.data_ptr(), ws.numel(), sol, stream) == 0
+        return y
+
+    first = run(-1)
+    close(first, ref)
+    assert torch.equal(run(-1), first)
+    assert torch.equal(run(10 ** 9), first)          # no such solution: heuristic first
+    buf = (ctypes.c_int * 16)()
+    n = hip.L.dd_gemm_bf16_solutions(M, N, K, ws.numel(), buf, 16)
+    assert 1 <= n <= 16
+    for sol in list(buf[:n]):
+        y = run(sol)
+        close(y, ref)
+        assert torch.equal(run(sol), y)
+    close(hip.linear(xc, wc), ref)
     # argument validation: nothing runs, hipErrorInvalidValue
+    y0 = torch.empty(M, N, dtype=BF, device="cuda")
     assert hip.L.dd_gemm_bf16(xc.data_ptr(), wc.data_ptr(), y0.data_ptr(), 0, N, K, ws.data_ptr(),
-                              ws.numel(), 1, stream) == 1
+                              ws.numel(), -1, stream) == 1
+    assert hip.L.dd_gemm_bf16_solutions(0, N, K, ws.numel(), buf, 16) == -1
 
 
 # ------------------------------------------------------------------------ qkv_post decode

@@ -54,3 +54,22 @@ def test_no_alloc_attention_matches_workspace_entry_point(cuda, shapes):
         got = _no_alloc(L, q, kc, vc, pos, B, W, NH, NKV, cap)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (B, W, cap)
+
+
+def test_no_alloc_first_call_under_capture(cuda):
+    """A fresh process whose first no-allocation call is made under graph capture: the call is
+    refused (hipErrorStreamCaptureUnsupported, 900) and records nothing; afterwards a call
+    outside capture, then the same call captured and replayed three times (eager work between
+    the replays), each equal bit for bit to dd_attn_decode with workspaces."""
+    import os
+    import subprocess
+    import sys
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture.py")
+    print("[no-alloc] first call under capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, child], capture_output=True, text=True, timeout=300)
+    line = [x for x in r.stdout.splitlines() if x.startswith("RESULT ")]
+    assert r.returncode == 0 and line, r.stderr[-2000:]
+    rc_first, untouched, rc_eager, eager_ok, rc_cap, replays_ok = map(int, line[0].split()[1:])
+    assert rc_first == 900 and untouched == 1
+    assert rc_eager == 0 and eager_ok == 1
+    assert rc_cap == 0 and replays_ok == 3
