@@ -250,7 +250,8 @@ def run_verify(torch, eng, prompts, W=5, steps=20):
 def run_spec(torch, eng, prompts, n, W):
     """End-to-end generate() of n tokens (prefill included, host loop included), plain greedy
     decode vs in-graph speculation at verify width W; each timed after one untimed warm-up
-    call. Returns (plain s, speculative s, verify steps, accepted drafts, identical tokens)."""
+    call. Returns (plain s, speculative s, verify steps, accepted drafts, plain tokens,
+    speculative tokens)."""
     sp = eng.speculator(W)
 
     def timed(fn):
@@ -264,7 +265,7 @@ def run_spec(torch, eng, prompts, n, W):
     tp, plain = timed(lambda: eng.generate(prompts, n))
     stats = {}
     ts, spec = timed(lambda: sp.generate(prompts, n, stats=stats))
-    return tp, ts, stats["steps"], stats["accepted_drafts"], plain == spec
+    return tp, ts, stats["steps"], stats["accepted_drafts"], plain, spec
 
 
 def run_prefill(torch, eng, prompts, reps=3, first=None):
@@ -482,6 +483,20 @@ def main():
             worst1, bad1, n1 = gap_check(eng, w1, toks1)
             extra["b1"]["gap_check"] = {"tokens": n1, "worst_gap": round(worst1, 4), "over_2": bad1}
             assert bad1 == 0, f"B=1: {bad1} emitted tokens exceed the 2-logit gap"
+            # greedy identity against the reference's torch arithmetic (untimed replay of the
+            # same generation keeping every step's logits; its tokens must be the timed run's)
+            from dryft_amd.teacher import decode_trace, token_identity
+            tr_toks, tr_logits = decode_trace(eng, w1, len(toks1))
+            assert [x[0] for x in tr_toks] == [x[0] for x in toks1], "replay differs from timed run"
+            ident = token_identity(eng, w1[0], [x[0] for x in toks1], tr_logits[:, 0])
+            del tr_logits
+            extra["b1"]["token_identity"] = dict(ident, path="vs the reference's torch arithmetic "
+                                                 "(hipBLASLt + SDPA) teacher-forced on prompt + "
+                                                 "emitted tokens; first_flip = first step off that "
+                                                 "path's own greedy run")
+            print(f"[bench] B=1 token identity: {ident['flips']} flips of {ident['tokens']} "
+                  f"(first {ident['first_flip']}), all near-ties {ident['all_near_ties']}, "
+                  f"worst logit diff {ident['worst_logit_diff']}", file=sys.stderr, flush=True)
         print(f"[bench] B=1: {ms1:.3f} ms/step, {1e3 / ms1:.0f} tok/s", file=sys.stderr, flush=True)
 
     if not args.no_verify:                    # configs[4] verify shape: W = 5 per row
@@ -495,13 +510,29 @@ def main():
 
     if not args.no_spec:                      # in-graph speculation, configs[3]'s B=1 shape
         p1 = [torch.randint(0, V, (128,), generator=g).tolist()]
-        tp, ts, nsteps, nacc, same = run_spec(torch, eng, p1, 512, 4)
+        tp, ts, nsteps, nacc, plain_t, spec_t = run_spec(torch, eng, p1, 512, 4)
+        same = plain_t == spec_t
+        div = None
+        if not same:
+            from dryft_amd.teacher import decode_trace, first_divergence_check
+            tr_toks, tr_logits = decode_trace(eng, p1, 512)
+            assert [x[0] for x in tr_toks] == [x[0] for x in plain_t]
+            div = first_divergence_check(eng, p1[0], [x[0] for x in plain_t], tr_logits[:, 0],
+                                         [x[0] for x in spec_t])
+            del tr_logits
         extra["speculative_b1"] = {
             "tokens": 512, "W": 4, "plain_tok_s": round(512 / tp, 1),
             "spec_tok_s": round(512 / ts, 1), "verify_steps": nsteps,
-            "accepted_drafts": nacc, "identical_to_plain": same,
+            "accepted_drafts": nacc, "identical_to_plain": same, "first_divergence": div,
             "note": "end-to-end generate() incl. prefill; random-init weights and prompt ids, so "
-                    "acceptance reflects this synthetic model's repetition, not natural text"}
+                    "acceptance reflects this synthetic model's repetition, not natural text. "
+                    "first_divergence: the first step where the speculative stream leaves the "
+                    "plain one, with both tokens' distance below the torch path's maximum there "
+                    "and the measured engine-vs-torch logit noise (near_tie: both within it)"}
+        if div is not None:
+            print(f"[bench] speculative stream leaves plain at step {div['step']}: "
+                  f"near_tie={div['near_tie']} (gaps {div['gap_plain']} / {div['gap_other']}, "
+                  f"noise {div['noise']})", file=sys.stderr, flush=True)
         print(f"[bench] speculative B=1 W=4: plain {512 / tp:.0f} tok/s, speculative "
               f"{512 / ts:.0f} tok/s ({nsteps} verify steps, {nacc} accepted drafts, "
               f"identical={same})", file=sys.stderr, flush=True)

@@ -61,3 +61,97 @@ def gap_check(eng, prompts, steps, tol=GAP_TOL):
         worst = max(worst, gap.max().item())
         bad += int((gap > tol).sum())
     return worst, bad, n * len(prompts)
+
+
+def _bf16_ulp(x):
+    import math
+    return 2.0 ** (math.floor(math.log2(max(abs(x), 2.0 ** -126))) - 7)
+
+
+@torch.inference_mode()
+def decode_trace(eng, prompts, n):
+    """Greedy decode of ``prompts`` for n tokens through the engine's captured step (the
+    product path), keeping every step's logits: returns (tokens [n][B], logits [n, B, V] bf16 on
+    the device; row t holds the logits that chose tokens[t], row 0 the prefill's)."""
+    B = len(prompts)
+    S = max(len(p) for p in prompts)
+    cap = -(-(S + n) // 128) * 128
+    st = eng._state(B, cap, graph=n > 1)
+    assert st.fused is not None, "decode_trace follows the one-launch decode step"
+    st.err.zero_()
+    V = eng.embed.shape[0]
+    logits = torch.empty((n, B, V), dtype=torch.bfloat16, device=eng.dev)
+    eng._dbg = []
+    try:
+        eng._prefill(prompts, st)
+        logits[0].copy_(eng._dbg[-1].to(eng.dev, torch.bfloat16))
+    finally:
+        eng._dbg = None
+    hist = torch.empty((n, B), dtype=torch.long, device=eng.dev)
+    hist[0].copy_(st.tok[:B])
+    for t in range(1, n):
+        if st.graph is not None:
+            st.graph.replay()
+        else:
+            eng._decode_body(st)
+        hist[t].copy_(st.tok[:B])
+        logits[t].copy_(st.fused.logits[:B])
+    torch.cuda.synchronize()
+    assert int(st.err.item()) == 0
+    return hist.cpu().tolist(), logits
+
+
+@torch.inference_mode()
+def token_identity(eng, prompt, toks, logits=None):
+    """Greedy token identity of one sequence's emitted tokens ``toks`` (list, toks[0] the
+    prefill's) against the reference's torch arithmetic teacher-forced on prompt + toks: a flip
+    is a token that is not that path's argmax. With the engine's own logits [n, V] (row t chose
+    toks[t]) each step's noise is max |engine - torch| over the vocabulary, and a flip is a
+    near-tie when the token's torch logit is below the torch maximum by no more than the larger
+    of 2 bf16 ulps and that noise (the two paths add in different orders, so candidates closer
+    than their disagreement may legitimately swap). Returns a dict: tokens, flips,
+    first_flip (the first step where the engine leaves the torch path's own greedy run, or
+    None), flip_detail [[step, gap, noise], ...], all_near_ties, worst_logit_diff."""
+    n = len(toks)
+    T = teacher_forced_logits(eng, list(prompt) + list(toks[:-1]), n)      # row t predicts toks[t]
+    t_ = torch.tensor(toks, device=T.device)
+    mx = T.max(-1).values
+    gap = (mx - T.gather(-1, t_[:, None])[:, 0]).cpu().tolist()
+    arg = T.argmax(-1).cpu().tolist()
+    noise = None
+    if logits is not None:
+        noise = (logits.float() - T).abs().max(-1).values.cpu().tolist()
+    mxl = mx.cpu().tolist()
+    detail, all_near = [], True
+    for t in range(n):
+        if toks[t] != arg[t]:
+            nz = noise[t] if noise is not None else 0.0
+            near = gap[t] <= max(2 * _bf16_ulp(mxl[t]), nz)
+            all_near = all_near and near
+            detail.append([t, round(gap[t], 5), round(nz, 5) if noise is not None else None])
+    return {"tokens": n, "flips": len(detail),
+            "first_flip": detail[0][0] if detail else None,
+            "flip_detail": detail[:32], "all_near_ties": all_near if noise is not None else None,
+            "worst_logit_diff": round(max(noise), 5) if noise is not None else None}
+
+
+@torch.inference_mode()
+def first_divergence_check(eng, prompt, plain, plain_logits, other):
+    """Where two emitted streams of one sequence part (``plain`` from the engine's decode step
+    with its logits, ``other`` e.g. the speculative path's): the first step t with
+    plain[t] != other[t], and whether both tokens there are acceptable greedy choices within the
+    measured noise: the torch path teacher-forced on the common prefix, each token's logit below
+    that path's maximum by no more than max(2 bf16 ulps, max |engine logits - torch logits| at
+    that step). Returns None when the streams are identical, else a dict."""
+    t = next((i for i, (a, b) in enumerate(zip(plain, other)) if a != b), None)
+    if t is None:
+        return None
+    T = teacher_forced_logits(eng, list(prompt) + list(plain[:t]), 1)[0]
+    noise = (plain_logits[t].float() - T).abs().max().item()
+    mx = T.max().item()
+    tol = max(2 * _bf16_ulp(mx), noise)
+    gp, go = mx - T[plain[t]].item(), mx - T[other[t]].item()
+    return {"step": t, "plain_token": plain[t], "other_token": other[t],
+            "gap_plain": round(gp, 5), "gap_other": round(go, 5),
+            "top2_margin": round(abs(T[plain[t]].item() - T[other[t]].item()), 5),
+            "noise": round(noise, 5), "near_tie": gp <= tol and go <= tol}
