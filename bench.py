@@ -584,8 +584,19 @@ def main():
     if not args.no_micro:
         extra["kv_layout"] = micro_kv_layout(torch, L, [n + 512 for n in lens])
         print(f"[bench] KV layout {extra['kv_layout']}", file=sys.stderr, flush=True)
-        extra["configs1_gemv"] = micro_gemv(torch, eng)
-        print(f"[bench] configs[1] {extra['configs1_gemv']}", file=sys.stderr, flush=True)
+        try:                                  # the product's GEMV phases, profiled alone
+            with open(os.path.join(ROOT, "profiles", "configs1_fused_phases.json")) as f:
+                extra["configs1"] = dict(json.load(f)["phases"],
+                                         source="profiles/configs1_fused_phases.json (rocprofv3 "
+                                                "kernel trace of phase_bench.py: each phase of the "
+                                                "one-launch step launched alone)")
+        except (OSError, ValueError, KeyError):
+            extra["configs1"] = None
+        extra["configs1_per_op_gemv"] = dict(micro_gemv(torch, eng),
+                                             path="dd_gemv, the per-op fallback for B > 16 and "
+                                                  "geometries the one-launch step does not take")
+        print(f"[bench] configs[1] per-op dd_gemv {extra['configs1_per_op_gemv']}", file=sys.stderr,
+              flush=True)
 
     roof = step_roofline(ms, bytes_step, B)
     print(f"[bench] roofline {roof}", file=sys.stderr, flush=True)

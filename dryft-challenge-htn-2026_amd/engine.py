@@ -233,13 +233,19 @@ class Engine:
         return sp
 
     def _select_spec(self, selftest):
-        """Speculation is opt-in (ENGINE_SPEC=1) and kept only if its generated tokens equal
-        plain greedy decode on a small case (engine.py:1057-1091: B=3, S=48, n=10, eager)."""
+        """Speculation is opt-in (ENGINE_SPEC=1) and kept only if the verify-shaped forward
+        matches sequential decode steps (engine.py:549-627, gate 0.5) and its generated tokens
+        equal plain greedy decode on a small case (engine.py:1057-1091: B=3, S=48, n=10, eager)."""
         if os.environ.get("ENGINE_SPEC", "0") != "1" or self.step is None:
             return None
         try:
             sp = self.speculator()
             if selftest:
+                d1, d2 = self._selftest_verify(sp.W)
+                print(f"[engine] verify selftest max logit diff: B=1 W=5 {d1:.4f}, "
+                      f"B=4 W={sp.W} at distinct positions {d2:.4f}")
+                if not (d1 <= 0.5 and d2 <= 0.5):
+                    return None
                 torch.manual_seed(3)
                 high = min(5000, self.embed.shape[0])
                 ids = torch.randint(min(100, high - 1), high, (3, 48)).tolist()
@@ -253,6 +259,56 @@ class Engine:
         except RuntimeError as ex:
             print(f"[engine] speculation unavailable: {ex}")
             return None
+
+    @torch.inference_mode()
+    def _selftest_verify(self, W2=4):
+        """engine.py:549-627: the verify-shaped forward against step-by-step decode on the
+        model's weights, two cases: B=1, W=5 at one position; B=4, W=W2 with each row's window at
+        a different offset (0, 3, 7, 11) into one lock-step decode timeline, so rows sit at
+        distinct positions (per-row position indexing). Returns the two max logit differences
+        (the reference's gate is 0.5)."""
+        torch.manual_seed(1)
+        high = min(5000, self.embed.shape[0])
+        low = min(100, high - 1)
+        dev = self.dev
+
+        def timeline(ids, B, S, n):
+            st = self._new_state(B, 128)
+            self._dbg = []
+            try:
+                self._prefill(ids, st)
+                toks = [st.tok.clone()]
+                for _ in range(n):
+                    self._decode_body(st)
+                    toks.append(st.tok.clone())
+                return st, toks, self._dbg
+            finally:
+                self._dbg = None
+
+        # B=1, W=5: row j is the token decode step j consumed, at position S + j
+        B, S, W = 1, 96, 5
+        ids = torch.randint(low, high, (B, S)).tolist()
+        _, toks, plain = timeline(ids, B, S, W)
+        sp = self._new_state(B, 128, W=W)
+        self._prefill(ids, sp)
+        got = self.verify_logits(sp, torch.stack(toks[:W], 1),
+                                 torch.full((B,), S, dtype=torch.long, device=dev)).float().cpu()
+        d1 = max((got[j] - plain[j + 1][0]).abs().max().item() for j in range(W))
+        # B=4, W=W2, rows at distinct positions of one lock-step timeline
+        B2, S2, offsets = 4, 96, (0, 3, 7, 11)
+        ids2 = torch.randint(low, high, (B2, S2)).tolist()
+        st2, toks2, plain2 = timeline(ids2, B2, S2, max(offsets) + W2)
+        sp2 = self._new_state(B2, 128, W=W2)
+        for i in range(self.L):
+            sp2.kc[i].copy_(st2.kc[i])
+            sp2.vc[i].copy_(st2.vc[i])
+        rows = torch.stack([torch.stack([toks2[o + s][b] for s in range(W2)])
+                            for b, o in enumerate(offsets)])
+        spos = torch.tensor([S2 + o for o in offsets], dtype=torch.long, device=dev)
+        got2 = self.verify_logits(sp2, rows, spos).float().cpu()
+        d2 = max((got2[b * W2 + s] - plain2[o + s + 1][b]).abs().max().item()
+                 for b, o in enumerate(offsets) for s in range(W2))
+        return d1, d2
 
     def _selftest(self, candidate, step=None):
         """engine.py:629-680 contract: prefill B=2, S=96, then 3 teacher-forced decode steps with

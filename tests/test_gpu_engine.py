@@ -115,6 +115,18 @@ def test_generate_raises_on_error_flag(tiny):
     assert list(eng.generate([[1, 2, 3]], 3))  # the flag is cleared by the next generate
 
 
+def test_verify_selftest_gate(tiny):
+    """The load-time verify check of speculation (engine.py:549-627): the verify-shaped forward
+    against step-by-step decode, B=1 W=5 and B=4 W=4 at distinct per-row positions, within the
+    reference's 0.5 gate."""
+    _, eng = tiny
+    if eng.step is None:
+        pytest.skip("per-op path: the verify check runs on the one-launch step")
+    d1, d2 = eng._selftest_verify(4)
+    print(f"verify selftest: B=1 W=5 {d1:.4f}, B=4 W=4 distinct positions {d2:.4f}")
+    assert d1 <= 0.5 and d2 <= 0.5
+
+
 @torch.inference_mode()
 def test_counters_recovered_after_barrier_timeout(tiny):
     """Recovery from a grid-barrier timeout of the one-launch step (error flag 4), forced from

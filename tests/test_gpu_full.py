@@ -400,6 +400,16 @@ def test_configs4_verify_w5(full):
           f"max excess over 2e-2 rel {deep:.4f}")
 
 
+def test_verify_selftest_full_size(full):
+    """The load-time verify check (engine.py:549-627) at full size: B=1 W=5, then B=4 W=4 with
+    rows at distinct positions of one decode timeline, against step-by-step decode; the
+    reference's gate is 0.5."""
+    _, _, eng = full
+    d1, d2 = eng._selftest_verify(4)
+    print(f"verify selftest (36 layers): B=1 W=5 {d1:.4f}, B=4 W=4 distinct positions {d2:.4f}")
+    assert d1 <= 0.5 and d2 <= 0.5
+
+
 @pytest.mark.timeout(900)
 @torch.inference_mode()
 def test_speculative_full_size(full):
