@@ -667,6 +667,16 @@ __device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
   return av > bv || (av == bv && ai < bi);
 }
 
+// am_better without short-circuit evaluation: the same result, as lane-mask arithmetic and one
+// select (the branching form compiles to divergent branches per value, which the 80-row lm_head,
+// with 100 candidates per lane, cannot afford)
+__device__ __forceinline__ bool am_better_nb(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv, lt = ai < bi;
+  const bool r_nan = an & (!bn | lt);
+  const bool r_num = (av > bv) | ((av == bv) & lt);
+  return (an | bn) ? r_nan : r_num;
+}
+
 template <int KIND, int NM, int EPI, bool STAGE>
 __device__ __forceinline__ void chunk_epilogue(const Args& a, Shared& sh, const Geo& g, int ch, int sp,
                                                int r, int rows, int ua, int oslot,
@@ -898,6 +908,41 @@ __device__ __forceinline__ int gemv_part(const Args& a) {
              : (int)blockIdx.x;
 }
 
+// 1/rms of every activation row of an 80-row step into sh.rs (MS = 16 NM rows): the rows'
+// sums of squares are [G][MS] per-workgroup partials. Thread t (t < SUBS * NRG) takes the 4
+// rows of row group t % NRG of the partials t / NRG + SUBS i, all requested before the first is
+// added; the SUBS subset sums then meet in LDS and are added in subset order.
+template <int NM>
+__device__ __forceinline__ void wide_rows_rsqrt(const Args& a, Shared& sh, const float* ss) {
+  constexpr int MS = 16 * NM;
+  constexpr int NRG = MS / 4, SUBS = NTHR / NRG, NIT = (MAXG + SUBS - 1) / SUBS, HALF = (NIT + 1) / 2;
+  const int rg = tid() % NRG, k = tid() / NRG;
+  const rsrc_t ssr = make_rsrc(ss, (unsigned)(gridDim.x * MS * 4));
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb) {
+    u32x4 v[HALF];
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      const int cw = k + SUBS * (hb * HALF + i);
+      v[i] = ldb128(ssr, k < SUBS && cw < (int)gridDim.x ? (unsigned)((cw * MS + 4 * rg) * 4) : OOB);
+    }
+#pragma unroll
+    for (int i = 0; i < HALF; ++i)
+      s += f32x4{__uint_as_float(v[i].x), __uint_as_float(v[i].y), __uint_as_float(v[i].z),
+                 __uint_as_float(v[i].w)};
+  }
+  float* part = &sh.u.g.red[0][0][0];      // [SUBS][MS] (the reduction buffer is free here)
+  if (k < SUBS) *(f32x4*)&part[k * MS + 4 * rg] = s;
+  lds_barrier();
+  if (tid() < MS) {
+    float v = 0.f;
+    for (int kk = 0; kk < SUBS; ++kk) v += part[kk * MS + tid()];
+    sh.rs[tid()] = rsqrt_ieee(v / (float)a.H + a.eps);
+  }
+  lds_barrier();
+}
+
 // One GEMV phase: arrive at the barrier (sync), start this phase's weight stream, wait, then
 // stream the activation with the remaining weights, one pass epilogue at a time.
 //   NORM: the input is rmsnorm(x) * lnw, 1/rms from the per-workgroup sums of squares `ss`
@@ -997,35 +1042,7 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
     lds_barrier();
     r[0] = sh.rs[tid() & 15];
   } else if (NORM) {
-    // NM > 1: [G][16 NM] partials of 16 NM rows. Thread t (t < SUBS * NRG) takes the 4 rows of
-    // row group t % NRG of the partials t / NRG + SUBS i, all requested before the first is
-    // added; the SUBS subset sums then meet in LDS and are added in subset order.
-    constexpr int NRG = MS / 4, SUBS = NTHR / NRG, NIT = (MAXG + SUBS - 1) / SUBS, HALF = (NIT + 1) / 2;
-    const int rg = tid() % NRG, k = tid() / NRG;
-    const rsrc_t ssr = make_rsrc(ss, (unsigned)(gridDim.x * MS * 4));
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      u32x4 v[HALF];
-#pragma unroll
-      for (int i = 0; i < HALF; ++i) {
-        const int cw = k + SUBS * (hb * HALF + i);
-        v[i] = ldb128(ssr, k < SUBS && cw < (int)gridDim.x ? (unsigned)((cw * MS + 4 * rg) * 4) : OOB);
-      }
-#pragma unroll
-      for (int i = 0; i < HALF; ++i)
-        s += f32x4{__uint_as_float(v[i].x), __uint_as_float(v[i].y), __uint_as_float(v[i].z),
-                   __uint_as_float(v[i].w)};
-    }
-    float* part = &sh.u.g.red[0][0][0];      // [SUBS][MS] (the reduction buffer is free here)
-    if (k < SUBS) *(f32x4*)&part[k * MS + 4 * rg] = s;
-    lds_barrier();
-    if (tid() < MS) {
-      float v = 0.f;
-      for (int kk = 0; kk < SUBS; ++kk) v += part[kk * MS + tid()];
-      sh.rs[tid()] = rsqrt_ieee(v / (float)a.H + a.eps);
-    }
-    lds_barrier();
+    wide_rows_rsqrt<NM>(a, sh, ss);
 #pragma unroll
     for (int n = 0; n < NM; ++n) r[n] = sh.rs[16 * n + (tid() & 15)];
   }
@@ -1066,6 +1083,224 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
     const rsrc_t ssr = make_rsrc(ss_slot<NM>(a, oslot), (unsigned)(gridDim.x * MS * 4));
     stc_f32(ssr, (unsigned)(blockIdx.x * MS + tid()) * 4, 0.f);
   }
+  STEP_TRACE(p, 3);
+}
+
+// ---------------------------------------------------------------------------------------------
+// lm_head of an 80-row step (NM > 1). The row-owned GEMV above splits a pass's k-steps over the
+// waves and reduces the waves' tile partials in LDS; with ~594 vocabulary rows per workgroup
+// (37 tiles) and 5 activation tiles per k-step its registers hold 4 weight tiles per pass, so
+// the lm_head took 10 passes, each re-reading and re-normalising the whole 80-row activation
+// (410 KB per CU per pass) and reducing 20 tile partials. Here the waves split the vocabulary
+// rows instead: wave w owns tiles w, w + 8, .. (LMW of them per round) over the whole K, so its
+// accumulators hold complete sums (no cross-wave reduction), and the normalised activation is
+// staged in LDS one stage of LMKC k-steps at a time, loaded and normalised once per workgroup
+// and round (one round when the tiles fit 8 LMW) and read by every wave from LDS. Each wave keeps
+// a ring of LMKC k-steps of its weight tiles in flight; the next stage's activation is loaded at
+// the start of a stage and normalised into the other LDS buffer at its end.
+#ifndef DD_V_LMW
+#define DD_V_LMW 5                            // vocabulary tiles per wave and round
+#endif
+#ifndef DD_V_LMKC
+#define DD_V_LMKC 3                           // k-steps per activation stage (= weight ring depth)
+#endif
+#ifndef DD_V_LM_WIDE
+#define DD_V_LM_WIDE 1
+#endif
+template <int NM>
+__device__ __forceinline__ void run_lm_wide(const Args& a, Shared& sh, int p, bool sync, unsigned epoch) {
+  constexpr int MS = 16 * NM, TW = DD_V_LMW, KC = DD_V_LMKC, CAPU = mat_CAPU(M_LM);
+  constexpr int NXI = (KC * MS * 4 + NTHR - 1) / NTHR;       // 16-byte staging items per thread
+  static_assert(2 * KC * MS * 64 + NWAVE * MS * 8 <= (int)sizeof(float) * NWAVE * RED_TILES * 256,
+                "staging buffers and argmax candidates fit the reduction buffer");
+  static_assert(MS * CAPU * 2 <= 2 * KC * MS * 64, "a chunk's logits fit the staging buffers");
+  const int K = a.H, M = a.M;
+  const Geo g = make_geo<M_LM, NM>(a.lm_t, a.V, K, (int)blockIdx.x);
+  const int lane = tid() & 63, wave = wave_id(), l16 = lane & 15, g4 = lane >> 4;
+  const int nk = g.nk, nst = (nk + KC - 1) / KC;
+  const int nt = g.nch > 0 ? (g.nch - 1) * (CAPU / 16) + (chunk_rows<M_LM>(g, g.nch - 1) + 15) / 16 : 0;
+  const int nround = (nt + NWAVE * TW - 1) / (NWAVE * TW);
+  const bf16* x = h_slot(a, 2 * a.L);
+  const rsrc_t xr = make_rsrc(x, (unsigned)((size_t)M * K * 2));
+  unsigned char* stg = (unsigned char*)&sh.u.g.red[0][0][0];   // [2][KC][MS][64 bytes]
+  float* candv = (float*)(stg + 2 * KC * MS * 64);             // [NWAVE][MS]
+  int* candi = (int*)(candv + NWAVE * MS);
+
+  // tile slot i of round rd: the lane's byte offset at k-step 0 and the per-k-step stride
+  unsigned wo[TW], wst[TW];
+  auto set_round = [&](int rd) {
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+      const int t = rd * NWAVE * TW + wave + NWAVE * i;
+      const int ch = t >> 3, tt = t & 7;
+      const int rows = t < nt ? chunk_rows<M_LM>(g, ch) : 0;
+      const int j = tt * 16 + l16;
+      wst[i] = (unsigned)rows * 64u;
+      wo[i] = j < rows ? (unsigned)(ch * CAPU) * (unsigned)K * 2u + (unsigned)j * 64u + (unsigned)g4 * 16u : OOB;
+    }
+  };
+  auto issue_w = [&](int ks, u32x4 (&w)[TW]) {
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+      w[i] = __builtin_amdgcn_raw_buffer_load_b128(g.wr, ks < nk && wo[i] != OOB ? wo[i] + (unsigned)ks * wst[i] : OOB,
+                                                    0u, CP_NT);
+  };
+  // activation stage s: item e = (k-step ks of the stage, row m, 16-byte quarter q)
+  auto stage_load = [&](int s, u32x4 (&v)[NXI]) {
+#pragma unroll
+    for (int i = 0; i < NXI; ++i) {
+      const int e = tid() + i * NTHR;
+      const int ksl = e / (MS * 4), rem = e - ksl * MS * 4, m = rem >> 2, q = rem & 3;
+      const int ks = s * KC + ksl;
+      v[i] = ldb128(xr, e < KC * MS * 4 && ks < nk && m < M ? (unsigned)((ks * M + m) * 64 + q * 16) : OOB);
+    }
+  };
+  auto stage_store = [&](int s, const u32x4 (&v)[NXI]) {
+    unsigned char* dst = stg + (s & 1) * KC * MS * 64;
+#pragma unroll
+    for (int i = 0; i < NXI; ++i) {
+      const int e = tid() + i * NTHR;
+      if (e < KC * MS * 4) {
+        const int ksl = e / (MS * 4), rem = e - ksl * MS * 4, m = rem >> 2, q = rem & 3;
+        const int ks = s * KC + ksl;
+        u32x4 y = {0u, 0u, 0u, 0u};
+        if (ks < nk) {
+          const float* wp = &sh.lnw[ks * 32 + q * 8];
+          y = norm8(v[i], sh.rs[m], *(const f32x4*)wp, *(const f32x4*)(wp + 4));
+        }
+        *(u32x4*)(dst + (ksl * MS + m) * 64 + q * 16) = y;
+      }
+    }
+  };
+
+  STEP_TRACE(p, 0);
+  if (sync) bar_arrive(a, epoch);
+  STEP_TRACE(p, 9);
+  const u32x4 lw = ldb128(make_rsrc(a.fnorm, (unsigned)(K * 2)), tid() * 8 < K ? (unsigned)(tid() * 16) : OOB);
+  u32x4 ring[KC][TW];
+  set_round(0);
+#pragma unroll
+  for (int j = 0; j < KC; ++j) issue_w(j, ring[j]);          // independent of the last phase
+  if (tid() * 8 < K) {
+    *(f32x4*)&sh.lnw[tid() * 8] = f32x4{lo_bf(lw.x), hi_bf(lw.x), lo_bf(lw.y), hi_bf(lw.y)};
+    *(f32x4*)&sh.lnw[tid() * 8 + 4] = f32x4{lo_bf(lw.z), hi_bf(lw.z), lo_bf(lw.w), hi_bf(lw.w)};
+  }
+  if (sync) bar_wait(a, sh, epoch);
+  STEP_TRACE(p, 1);
+  wide_rows_rsqrt<NM>(a, sh, ss_slot<NM>(a, 2 * a.L));        // sh.rs; ends with a barrier
+  STEP_TRACE(p, 2);
+  float bv[NM];
+  int bi[NM];
+#pragma unroll
+  for (int n = 0; n < NM; ++n) {
+    bv[n] = -INFINITY;
+    bi[n] = 0x7fffffff;
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+    if (rd > 0) {
+      set_round(rd);
+#pragma unroll
+      for (int j = 0; j < KC; ++j) issue_w(j, ring[j]);
+    }
+    {
+      u32x4 v[NXI];
+      stage_load(0, v);
+      stage_store(0, v);
+    }
+    __syncthreads();
+    f32x4 acc[TW][NM];
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+      for (int n = 0; n < NM; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nst; ++s) {
+      u32x4 v[NXI];
+      if (s + 1 < nst) stage_load(s + 1, v);
+      const unsigned char* src = stg + (s & 1) * KC * MS * 64;
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        u32x4 xv[NM];
+#pragma unroll
+        for (int n = 0; n < NM; ++n) xv[n] = *(const u32x4*)(src + (j * MS + 16 * n + l16) * 64 + g4 * 16);
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+#pragma unroll
+          for (int n = 0; n < NM; ++n) acc[i][n] = mfma16x16x32(ring[j][i], xv[n], acc[i][n]);
+        issue_w((s + 1) * KC + j, ring[j]);                    // past nk: reads zeros
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (s + 1 < nst) stage_store(s + 1, v);
+      __syncthreads();
+    }
+    STEP_TRACE(p, 7);
+    // Logits of the round, one tile slot at a time: the 8 waves' tiles of slot i are chunk
+    // rd TW + i (tile t = chunk 8 t + wave), so they meet in LDS as [row][128 columns] (the
+    // staging buffers are free now) and go out as row-contiguous runs (lane-consecutive
+    // columns); each lane also keeps a running argmax per activation row of its own values.
+    bf16* lgb = (bf16*)stg;                                     // [MS][CAPU]
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+      const int ch = rd * TW + i;
+      const int rows = ch < g.nch ? chunk_rows<M_LM>(g, ch) : 0;
+#pragma unroll
+      for (int n = 0; n < NM; ++n) {
+        const int m = 16 * n + l16;
+        unsigned pk[2];
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+          const bf16 b0 = f2bf(acc[i][n][q]), b1 = f2bf(acc[i][n][q + 1]);
+          pk[q >> 1] = (unsigned)b0 | ((unsigned)b1 << 16);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int j = wave * 16 + g4 * 4 + q + h;
+            const int col = g.u0 + ch * CAPU + j;
+            const float fv = bf2f(h ? b1 : b0);
+            const bool up = (m < M) & (j < rows) & am_better_nb(fv, col, bv[n], bi[n]);
+            bv[n] = up ? fv : bv[n];
+            bi[n] = up ? col : bi[n];
+          }
+        }
+        *(u32x2*)&lgb[m * CAPU + wave * 16 + g4 * 4] = u32x2{pk[0], pk[1]};
+      }
+      lds_barrier();
+      const int nr = rows > 0 ? M * rows : 0;
+      bf16* out = a.logits + g.u0 + ch * CAPU;
+      for (int e = tid(); e < nr; e += NTHR) {
+        const int m = e / rows, j = e - m * rows;
+        out[(size_t)m * a.V + j] = lgb[m * CAPU + j];
+      }
+      lds_barrier();
+    }
+  }
+  // the lanes of a row (l16 + 16 g4) meet by shuffles, the waves in LDS
+#pragma unroll
+  for (int n = 0; n < NM; ++n) {
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+      const float ov = __shfl_xor(bv[n], o, 64);
+      const int oi = __shfl_xor(bi[n], o, 64);
+      const bool up = am_better_nb(ov, oi, bv[n], bi[n]);
+      bv[n] = up ? ov : bv[n];
+      bi[n] = up ? oi : bi[n];
+    }
+    if (g4 == 0) {
+      candv[wave * MS + 16 * n + l16] = bv[n];
+      candi[wave * MS + 16 * n + l16] = bi[n];
+    }
+  }
+  lds_barrier();
+  if (tid() < M) {
+    float v = sh.bestv[tid()];
+    int ix = sh.besti[tid()];
+    for (int w = 0; w < NWAVE; ++w)
+      if (am_better_nb(candv[w * MS + tid()], candi[w * MS + tid()], v, ix)) {
+        v = candv[w * MS + tid()];
+        ix = candi[w * MS + tid()];
+      }
+    sh.bestv[tid()] = v;
+    sh.besti[tid()] = ix;
+  }
+  lds_barrier();
   STEP_TRACE(p, 3);
 }
 
@@ -2111,8 +2346,11 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
   const int qlm = 1 + 5 * a.L;
   if (in_range(qlm)) {
     SET_PHASE(qlm);
-    run_gemv<M_LM, NM, true, EPI_LOGITS>(a, sh, qlm, qlm > a.phase_begin, epoch_of(qlm), a.lm_t, a.V,
-                                         a.H, h_slot(a, 2 * a.L), a.fnorm, ss_slot<NM>(a, 2 * a.L), 0);
+    if (NM > 1 && DD_V_LM_WIDE)
+      run_lm_wide<NM>(a, sh, qlm, qlm > a.phase_begin, epoch_of(qlm));
+    else
+      run_gemv<M_LM, NM, true, EPI_LOGITS>(a, sh, qlm, qlm > a.phase_begin, epoch_of(qlm), a.lm_t, a.V,
+                                           a.H, h_slot(a, 2 * a.L), a.fnorm, ss_slot<NM>(a, 2 * a.L), 0);
     // argmax over the workgroups' candidates; the last workgroup writes the tokens and, for a
     // decode step (W = 1), advances the positions
     const rsrc_t cr = make_rsrc(a.ws + a.off_am, (unsigned)(gridDim.x * MS * 2 * 4));
