@@ -366,6 +366,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// The value of lane l ^ 16 (l ^ 32) through gfx950's v_permlane16_swap (v_permlane32_swap)
+// instead of an LDS round trip (ds_bpermute, which __shfl_xor compiles to): swapping a register
+// with itself leaves each lane the pair (value of the lower row, value of the upper row).
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((tid() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((tid() & 32) ? r[0] : r[1]);
+}
+
 // Transposing LDS read of four 16-bit elements (gfx950 ds_read_b64_tr_b16), per 16-lane group:
 // output lane j receives element j % 4 of the 8-byte rows that source lanes j / 4, j / 4 + 4,
 // j / 4 + 8, j / 4 + 12 address (in that order, low half first). `p` is 8-byte aligned LDS.
@@ -2075,8 +2087,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
               sv[t * 4 + q] = v;
               mloc = fmaxf(mloc, v);
             }
-          mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-          mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+          // (the two-tile instantiation keeps the LDS shuffles: its register allocation spills more
+          // with the swaps)
+          mloc = fmaxf(mloc, NQT == 1 ? lane_xor16(mloc) : __shfl_xor(mloc, 16, 64));
+          mloc = fmaxf(mloc, NQT == 1 ? lane_xor32(mloc) : __shfl_xor(mloc, 32, 64));
           const float m_new = fmaxf(m_run[qt], mloc);
           const float msafe = m_new == -INFINITY ? 0.f : m_new;
           alpha[qt] = exp2f(m_run[qt] - msafe);
@@ -2089,8 +2103,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
             psum += pa + pb;
             pk[jj] = pk_bf16(pa, pb);
           }
-          psum += __shfl_xor(psum, 16, 64);
-          psum += __shfl_xor(psum, 32, 64);
+          psum += NQT == 1 ? lane_xor16(psum) : __shfl_xor(psum, 16, 64);
+          psum += NQT == 1 ? lane_xor32(psum) : __shfl_xor(psum, 32, 64);
           l_run[qt] = l_run[qt] * alpha[qt] + psum;
           m_run[qt] = m_new;
           pB[qt] = u32x4{pk[0], pk[1], pk[2], pk[3]};
