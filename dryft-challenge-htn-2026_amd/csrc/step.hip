@@ -378,6 +378,20 @@ __device__ __forceinline__ float lane_xor32(float v) {
   return __uint_as_float((tid() & 32) ? r[0] : r[1]);
 }
 
+// 0 + x[0] + x[1] + .. + x[7] (in that order) for x[w] = p[w * stride] in LDS, the eight loads
+// issued together: left to itself the register-bound scheduler waits for each load (or pair)
+// before issuing the next, one LDS round trip per wave's partial.
+__device__ __forceinline__ float lds_sum8(const float* p, int stride) {
+  float x[NWAVE];
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) x[w] = p[w * stride];
+  __builtin_amdgcn_sched_barrier(0);
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) v += x[w];
+  return v;
+}
+
 // Transposing LDS read of four 16-bit elements (gfx950 ds_read_b64_tr_b16), per 16-lane group:
 // output lane j receives element j % 4 of the 8-byte rows that source lanes j / 4, j / 4 + 4,
 // j / 4 + 8, j / 4 + 12 address (in that order, low half first). `p` is 8-byte aligned LDS.
@@ -739,9 +753,7 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
     for (int e = tid(); e < RT * NM * 256; e += NTHR) {
       const int tn = e >> 8, ln = (e >> 2) & 63, q = e & 3;
       const int i = tn / NM, n = tn - i * NM;
-      float s = 0.f;
-#pragma unroll
-      for (int w = 0; w < NWAVE; ++w) s += sh.u.g.red[w][tn][e & 255];
+      const float s = lds_sum8(&sh.u.g.red[0][tn][e & 255], RED_TILES * 256);
       sh.u.g.res[(i * 16 + (ln >> 4) * 4 + q) * RW + 16 * n + (ln & 15)] = s;
     }
     lds_barrier();
@@ -1056,9 +1068,7 @@ __device__ __forceinline__ void run_gemv(const Args& a, Shared& sh, int p, bool 
     }
     lds_barrier();
     if (tid() < 16) {
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < NWAVE; ++w) v += sh.rsp[w][tid()];
+      const float v = lds_sum8(&sh.rsp[0][tid()], MAXROWS);
       sh.rs[tid()] = rsqrt_ieee(v / (float)a.H + a.eps);
     }
     lds_barrier();
@@ -1481,9 +1491,7 @@ __device__ __forceinline__ void run_res_split(const Args& a, Shared& sh, int p, 
   for (int e = tid(); e < 2 * NM * 256; e += NTHR) {
     const int tn = e >> 8, ln = (e >> 2) & 63, i = e & 3;
     const int t = tn / NM, n = tn - t * NM;
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) v += sh.u.g.red[w][tn][e & 255];
+    const float v = lds_sum8(&sh.u.g.red[0][tn][e & 255], RED_TILES * 256);
     sh.u.g.res[(t * 16 + (ln >> 4) * 4 + i) * RW + 16 * n + (ln & 15)] = v;
   }
   lds_barrier();
