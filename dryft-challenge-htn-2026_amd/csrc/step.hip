@@ -2125,35 +2125,20 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // V^T operand of dim tile dt: lane (l16, g4) needs V[key][dt 16 + l16] for keys g4 4 + q
-        // and 16 + g4 4 + q (q = 0..3, the lane-local P key order). With one query tile these are
-        // two transposing LDS loads (ds_read_b64_tr_b16: output lane j of a 16-lane group gets
-        // element j % 4 of the 8-byte rows that source lanes j / 4 + 4 q address), each source
-        // lane addressing 4 dims of one key: 16 loads per block instead of 64 two-byte loads,
-        // which the register-bound compiler issued two at a time, each pair waited for (decode
-        // B = 16 2.661 -> 2.617 ms, B = 1 1.975 -> 1.954). The two-tile instantiation keeps the
-        // two-byte loads (4.820 -> 4.880 ms per verify step with the transposing loads).
-        if (NQT == 1) {
-          const int trow = g4 * 4 + (l16 >> 2), tcol = 4 * (l16 & 3);
+        // and 16 + g4 4 + q (q = 0..3, the lane-local P key order): two transposing LDS loads
+        // (ds_read_b64_tr_b16: output lane j of a 16-lane group gets element j % 4 of the 8-byte
+        // rows that source lanes j / 4 + 4 q address), each source lane addressing 4 dims of one
+        // key. 16 loads per block instead of 64 two-byte loads, which the register-bound compiler
+        // issued two at a time, each pair waited for (decode B = 16 2.661 -> 2.617 ms, B = 1
+        // 1.975 -> 1.954; verify 4.794 -> 4.781).
+        const int trow = g4 * 4 + (l16 >> 2), tcol = 4 * (l16 & 3);
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            const u32x2 lo = lds_read_tr16(&vs[trow][dt * 16 + tcol]);
-            const u32x2 hi = lds_read_tr16(&vs[16 + trow][dt * 16 + tcol]);
-            acc[0][dt] = mfma16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pB[0], acc[0][dt]);
-          }
-        } else {
+        for (int dt = 0; dt < 8; ++dt) {
+          const u32x2 lo = lds_read_tr16(&vs[trow][dt * 16 + tcol]);
+          const u32x2 hi = lds_read_tr16(&vs[16 + trow][dt * 16 + tcol]);
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            const int d = dt * 16 + l16;
-            unsigned av[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              const int ka = (jj < 2) ? (g4 * 4 + 2 * jj) : (16 + g4 * 4 + 2 * (jj - 2));
-              av[jj] = (unsigned)vs[ka][d] | ((unsigned)vs[ka + 1][d] << 16);
-            }
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt)
-              acc[qt][dt] = mfma16x16x32(u32x4{av[0], av[1], av[2], av[3]}, pB[qt], acc[qt][dt]);
-          }
+          for (int qt = 0; qt < NQT; ++qt)
+            acc[qt][dt] = mfma16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pB[qt], acc[qt][dt]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
