@@ -464,6 +464,7 @@ __device__ __forceinline__ void bar_wait(const Args& a, Shared& sh, unsigned epo
         break;
       }
     }
+    STEP_TRACE(a.phase_cur, 11);             // the poller saw the release
   } else if (wave_id() == 0 && !sh.bail) {
     const int lane = tid() & 63;
     const unsigned target = epoch * (unsigned)(gridDim.x >> 3);
@@ -1870,6 +1871,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       pre = wave < ns && !(before_wait && wave < DD_ATT_NOPRE);   // wave 0 polls the barrier
       if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
     }
+    if (before_wait) STEP_TRACE_WAVE(p, 12);   // the wave's pre-wait requests issued
     return pre;
   };
   bool pre = start_round(i0, sync);                // kreg/vreg hold the wave's next block
@@ -2144,7 +2146,6 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      if (sg == 0) STEP_TRACE_WAVE(p, 12);     // this wave's blocks of the first segment done
       // the waves' running max and sum of every query row
       if (g4 == 0) {
 #pragma unroll
