@@ -20,6 +20,7 @@ import glob
 import json
 import math
 import os
+import sys
 
 import torch
 
@@ -192,7 +193,8 @@ class Engine:
                 break
             try:
                 diff = self._selftest(cand)
-                print(f"[engine] HIP ops {label} selftest max logit diff {diff:.4f}")
+                print(f"[engine] HIP ops {label} selftest max logit diff {diff:.4f}",
+                      file=sys.stderr)
                 if diff <= 0.5:
                     ops = cand
                     break
@@ -215,13 +217,14 @@ class Engine:
         try:
             step = FusedStep(self)
         except RuntimeError as ex:
-            print(f"[engine] fused decode step unavailable: {ex}")
+            print(f"[engine] fused decode step unavailable: {ex}", file=sys.stderr)
             return None
         if selftest:
             diff = self._selftest(self.ops, step)
-            print(f"[engine] fused decode step selftest max logit diff {diff:.4f}")
+            print(f"[engine] fused decode step selftest max logit diff {diff:.4f}", file=sys.stderr)
             if not diff <= 0.5:
-                print("[engine] fused decode step failed its self-test; using per-op kernels")
+                print("[engine] fused decode step failed its self-test; using per-op kernels",
+                      file=sys.stderr)
                 return None
         return step
 
@@ -243,7 +246,7 @@ class Engine:
             if selftest:
                 d1, d2 = self._selftest_verify(sp.W)
                 print(f"[engine] verify selftest max logit diff: B=1 W=5 {d1:.4f}, "
-                      f"B=4 W={sp.W} at distinct positions {d2:.4f}")
+                      f"B=4 W={sp.W} at distinct positions {d2:.4f}", file=sys.stderr)
                 if not (d1 <= 0.5 and d2 <= 0.5):
                     return None
                 torch.manual_seed(3)
@@ -252,12 +255,13 @@ class Engine:
                 plain = list(self.generate(ids, 10))
                 got = list(sp.generate(ids, 10, graph=False))
                 self.states.clear()
-                print(f"[engine] speculative selftest B=3 S=48 n=10 W={sp.W} match={got == plain}")
+                print(f"[engine] speculative selftest B=3 S=48 n=10 W={sp.W} match={got == plain}",
+                      file=sys.stderr)
                 if got != plain:
                     return None
             return sp
         except RuntimeError as ex:
-            print(f"[engine] speculation unavailable: {ex}")
+            print(f"[engine] speculation unavailable: {ex}", file=sys.stderr)
             return None
 
     @torch.inference_mode()
@@ -383,7 +387,7 @@ class Engine:
             try:
                 self._capture(st)
             except Exception as e:  # fall back to eager decode (engine.py:365-370)
-                print(f"[engine] graph capture failed for {key}: {e!r}")
+                print(f"[engine] graph capture failed for {key}: {e!r}", file=sys.stderr)
                 st.graph = None
         return st
 

@@ -20,6 +20,8 @@ Gate (engine.py:51, 61-64, 693-706): 1 <= B <= 8 and n >= 64, and the one-launch
 B x W rows; the engine turns speculation on only when ENGINE_SPEC=1 and the load-time check
 (tokens identical to plain decode, engine.py:1057-1091) passes.
 """
+import sys
+
 import torch
 
 from ._lib import check, lib
@@ -73,7 +75,8 @@ class Speculator:
             try:
                 self._capture(st)
             except Exception as ex:  # eager replays instead (engine.py:365-370 contract)
-                print(f"[engine] speculative graph capture failed for {key}: {ex!r}")
+                print(f"[engine] speculative graph capture failed for {key}: {ex!r}",
+                      file=sys.stderr)
                 st.graph = None
         return st
 
