@@ -1624,6 +1624,9 @@ __host__ __device__ constexpr int att_ovh(int B, int W) {
 #ifndef DD_ATT_NOPRE
 #define DD_ATT_NOPRE 1               // waves 0 .. n-1 request no K/V block before the barrier wait
 #endif
+#ifndef DD_ATT_KPRE
+#define DD_ATT_KPRE 1                // K half of the first block before the wait (see below)
+#endif
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
 // keys that exist for sequence b this step (its cache below pos plus its W new tokens)
@@ -1822,7 +1825,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   // one 32-key block of K (S^T operand: lane = key l16 of half t, dims kb*32 + g4*8) and V
   // (rows of 16 keys x 8 dims, transposed through LDS below)
   u32x4 kreg[2][4], vreg[8];
-  auto load_block = [&](size_t kvbase, int key0) {
+  auto load_k = [&](size_t kvbase, int key0) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       int key = key0 + t * 16 + l16;
@@ -1830,6 +1833,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) kreg[t][kb] = ld16(kc + kvbase + (size_t)key * HD + kb * 32 + g4 * 8);
     }
+  };
+  auto load_v = [&](size_t kvbase, int key0) {
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int cc = it * 64 + lane;
@@ -1838,6 +1843,19 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
       vreg[it] = ld16(vc + kvbase + (size_t)key * HD + (cc & 15) * 8);
     }
   };
+  auto load_block = [&](size_t kvbase, int key0) {
+    load_k(kvbase, key0);
+    load_v(kvbase, key0);
+  };
+  // One query tile and the XCD-local wait (B >= 3): before the barrier wait the waves request
+  // only the K half of their first block, its V half after the prologue. The full blocks (112 KB
+  // per CU) take ~4 us to issue when every CU requests at once; the last wave to finish issuing
+  // set the release (s_barrier) at 6.5 us after the XCD's last QKV arrival, the poller having
+  // seen it at 2.0 us (trace build: release 6.3 -> 3.8 us, attention span 27.7 -> 26.7 us per
+  // layer; step B = 16 2.589 -> 2.579 ms. B = 1, whose few attention workgroups are not issue
+  // bound, measured 1.928 -> 1.950 with the split and keeps whole blocks.)
+  const bool KPRE = DD_ATT_KPRE && NQT == 1 && P == 8;
+  bool vpend = false;
   // ---- a round's segments: (sequence, kv head) pairs whose blocks meet [i, i1), then the wave's
   // first block of the round's first segment (its latency overlaps the prologue; before the
   // barrier wait wave 0, the poller, requests nothing so its poll is not queued behind a block)
@@ -1869,7 +1887,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
     if (sh.nseg > 0) {
       const int b = sh.seg[0][0], kvh = sh.seg[0][1], j0 = sh.seg[0][2], ns = sh.seg[0][3];
       pre = wave < ns && !(before_wait && wave < DD_ATT_NOPRE);   // wave 0 polls the barrier
-      if (pre) load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
+      if (pre) {
+        if (KPRE && before_wait) {
+          load_k((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
+          vpend = true;
+        } else {
+          load_block((size_t)(b * NKV + kvh) * a.cap * HD, (j0 + wave) * 32);
+        }
+      }
     }
     if (before_wait) STEP_TRACE_WAVE(p, 12);   // the wave's pre-wait requests issued
     return pre;
@@ -1993,6 +2018,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         dst[lane] = f2bf(x0);
         dst[lane + 64] = f2bf(x1);
       }
+    }
+    if (vpend) {                                // the first block's V half (see KPRE above)
+      load_v((size_t)(sh.seg[0][0] * NKV + sh.seg[0][1]) * a.cap * HD, (sh.seg[0][2] + wave) * 32);
+      vpend = false;
     }
     lds_barrier();
     if (first_seg) STEP_TRACE(p, 5);
