@@ -1853,7 +1853,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
   // set the release (s_barrier) at 6.5 us after the XCD's last QKV arrival, the poller having
   // seen it at 2.0 us (trace build: release 6.3 -> 3.8 us, attention span 27.7 -> 26.7 us per
   // layer; step B = 16 2.589 -> 2.579 ms. B = 1, whose few attention workgroups are not issue
-  // bound, measured 1.928 -> 1.950 with the split and keeps whole blocks.)
+  // bound, measured 1.928 -> 1.950 with the split and keeps whole blocks; so does the two-tile
+  // instantiation: 4.788 -> 4.927 ms per verify step with the split.)
   const bool KPRE = DD_ATT_KPRE && NQT == 1 && P == 8;
   bool vpend = false;
   // ---- a round's segments: (sequence, kv head) pairs whose blocks meet [i, i1), then the wave's
