@@ -273,13 +273,13 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       const float m_new = fmaxf(m_run[h], mloc);
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run[h] - msafe);
+      const float alpha = exp2_hw(m_run[h] - msafe);
       float psum = 0.f;
       unsigned pk[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const float pa = exp2f(sv[2 * jj] - msafe);
-        const float pb = exp2f(sv[2 * jj + 1] - msafe);
+        const float pa = exp2_hw(sv[2 * jj] - msafe);
+        const float pb = exp2_hw(sv[2 * jj + 1] - msafe);
         psum += pa + pb;
         pk[jj] = pk_bf16(pa, pb);
       }
