@@ -149,13 +149,13 @@ attn_decode_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc,
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       const float m_new = fmaxf(m_run[rb], mloc);
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run[rb] - msafe);
+      const float alpha = exp2_hw(m_run[rb] - msafe);
       float psum = 0.f;
       unsigned pk[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float pa = exp2f(sv[2 * j] - msafe);
-        const float pb = exp2f(sv[2 * j + 1] - msafe);
+        const float pa = exp2_hw(sv[2 * j] - msafe);
+        const float pb = exp2_hw(sv[2 * j + 1] - msafe);
         psum += pa + pb;
         pk[j] = (unsigned)f2bf(pa) | ((unsigned)f2bf(pb) << 16);
       }
@@ -214,7 +214,7 @@ attn_decode_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc,
       float o = 0.f, l = 0.f;
 #pragma unroll
       for (int w = 0; w < ATT_WAVES; ++w) {
-        const float f = exp2f(sh.ms[w][rr] - Ms);
+        const float f = exp2_hw(sh.ms[w][rr] - Ms);
         o += sh.u.mrg[w][rr][d] * f;
         l += sh.ls[w][rr] * f;
       }
@@ -244,7 +244,7 @@ attn_decode_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc,
     float o = 0.f, l = 0.f;
     for (int sp = 0; sp < nsplit; ++sp) {
       const unsigned ps = p + sp * sstride;
-      const float f = exp2f(ldc_f32(wsr, ps + HD * 4) - M);
+      const float f = exp2_hw(ldc_f32(wsr, ps + HD * 4) - M);
       o += ldc_f32(wsr, ps + d * 4) * f;
       l += ldc_f32(wsr, ps + (HD + 1) * 4) * f;
     }

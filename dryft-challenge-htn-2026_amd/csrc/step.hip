@@ -1756,7 +1756,7 @@ __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, in
       for (int j = 0; j < ATT_CB; ++j) {
         if (mv[j] == -INFINITY) continue;
         const float Mn = fmaxf(Mx, mv[j]);
-        const float fo = exp2f(Mx - Mn), fn = exp2f(mv[j] - Mn);
+        const float fo = exp2_hw(Mx - Mn), fn = exp2_hw(mv[j] - Mn);
         o = o * fo + ov[j] * fn;
         l = l * fo + lv[j] * fn;
         Mx = Mn;
@@ -2133,13 +2133,13 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
           mloc = fmaxf(mloc, NQT == 1 ? lane_xor32(mloc) : __shfl_xor(mloc, 32, 64));
           const float m_new = fmaxf(m_run[qt], mloc);
           const float msafe = m_new == -INFINITY ? 0.f : m_new;
-          alpha[qt] = exp2f(m_run[qt] - msafe);
+          alpha[qt] = exp2_hw(m_run[qt] - msafe);
           float psum = 0.f;
           unsigned pk[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const float pa = exp2f(sv[2 * jj] - msafe);
-            const float pb = exp2f(sv[2 * jj + 1] - msafe);
+            const float pa = exp2_hw(sv[2 * jj] - msafe);
+            const float pb = exp2_hw(sv[2 * jj + 1] - msafe);
             psum += pa + pb;
             pk[jj] = pk_bf16(pa, pb);
           }
@@ -2229,7 +2229,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
           float o = 0.f, l = 0.f;
 #pragma unroll
           for (int w = 0; w < NWAVE; ++w) {
-            const float f = exp2f(mv[w] - Ms);
+            const float f = exp2_hw(mv[w] - Ms);
             o += ov[w] * f;
             l += lv[w] * f;
           }
