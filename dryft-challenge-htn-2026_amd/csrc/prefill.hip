@@ -39,6 +39,18 @@ constexpr int VROW = KB + 4;           // LDS V^T row (elements): 72 bytes (18 w
                                        // dim rows one staging store spans fall in 4 disjoint
                                        // 16-bank ranges)
 
+// The value of lane l ^ 16 (l ^ 32) through gfx950's v_permlane16_swap (v_permlane32_swap), a
+// VALU operation, instead of the LDS round trip (ds_bpermute) __shfl_xor compiles to: swapping a
+// register with itself leaves each lane the pair (value of the lower row, value of the upper row).
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // prompt and position of packed token t (seq_start: B + 1 ascending offsets)
 __device__ __forceinline__ void locate(const int* __restrict__ seq_start, int B, int t, int& b, int& p) {
   int lo = 0, hi = B - 1;
@@ -269,8 +281,8 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
           sv[t * 4 + i] = v;
           mloc = fmaxf(mloc, v);
         }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = fmaxf(mloc, lane_xor16(mloc));
+      mloc = fmaxf(mloc, lane_xor32(mloc));
       const float m_new = fmaxf(m_run[h], mloc);
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = exp2_hw(m_run[h] - msafe);
@@ -283,8 +295,8 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
         psum += pa + pb;
         pk[jj] = pk_bf16(pa, pb);
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
+      psum += lane_xor16(psum);
+      psum += lane_xor32(psum);
       l_run[h] = l_run[h] * alpha + psum;
       m_run[h] = m_new;
       const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
