@@ -4,9 +4,9 @@
 // holding tokens seq_start[b] .. seq_start[b+1] - 1 at positions 0 .. len_b - 1, so a ragged
 // batch prefills in one launch per kernel instead of one pass per prompt length.
 //
-// qkv_prefill_kernel: one workgroup of 4 waves per token, a wave per head in turn (the raw heads
-// of a batch of 8 requested together); lane l holds dims 2l and 2l + 1 (4-byte accesses), its
-// rotate-half partners in lane l ^ 32. Rounding points as the reference's
+// qkv_prefill_kernel: one workgroup per 16 tokens, a 16-lane group per token taking its heads in
+// turn (the raw heads of a batch of 8 requested together); lane j holds dims 4j .. 4j + 3 and
+// their rotate-half partners 64 + 4j .. (two 8-byte accesses). Rounding points as the reference's
 // (engine.py:107-115, 166-187; fused.py:191-200, 221-257):
 //   n = bf16(bf16(x * r) * w), r = 1/sqrt(mean(x^2) + eps)
 //   out[d]    = bf16(bf16(n[d] * cos[d]) + bf16(-n[d+64] * sin[d]))        d < 64
@@ -63,65 +63,96 @@ __device__ __forceinline__ void locate(const int* __restrict__ seq_start, int B,
   p = t - seq_start[lo];
 }
 
-// heads of one wave whose loads are in flight together (a wave takes heads wave, wave + 4, ..)
-constexpr int QKV_HPB = 8;
+// One workgroup per 16 tokens: each 16-lane group takes one token's heads in turn, QKV_HPB heads'
+// loads in flight together. Lane j of a group holds dims 4j .. 4j + 3 and 64 + 4j .. 64 + 4j + 3
+// (two 8-byte accesses), so both rotate-half partners of every dim are in the lane; the head's
+// sum of squares is the lane's 8 squares added in order, then reduced over the 16 lanes.
+constexpr int QKV_TPW = 16;            // tokens per workgroup (4 waves x 4 groups)
+#ifndef DD_QKV_HPB
+#define DD_QKV_HPB 8
+#endif
+constexpr int QKV_HPB = DD_QKV_HPB;
+
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 
 __global__ void __launch_bounds__(256)
 qkv_prefill_kernel(const bf16* __restrict__ qkv, const bf16* __restrict__ qn,
                    const bf16* __restrict__ kn, const bf16* __restrict__ cos_t,
-                   const bf16* __restrict__ sin_t, const int* __restrict__ seq_start, int B,
+                   const bf16* __restrict__ sin_t, const int* __restrict__ seq_start, int B, int T,
                    int last_only, bf16* __restrict__ q_out, bf16* __restrict__ kc,
                    bf16* __restrict__ vc, int NH, int NKV, int cap, int rope_rows, float eps,
                    int* __restrict__ err) {
-  const int t = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15;
+  const int t = blockIdx.x * QKV_TPW + wave * 4 + (lane >> 4);   // this group's token
+  if (t >= T) return;                                             // whole group
   int b, p;
   locate(seq_start, B, t, b, p);
   const int len = seq_start[b + 1] - seq_start[b];
   if (p < 0 || p >= len || p >= cap || p >= rope_rows) {   // never write outside the cache
-    if (threadIdx.x == 0 && err != nullptr) atomicOr(err, 2);
+    if (j == 0 && err != nullptr) atomicOr(err, 2);
     return;
   }
   // last_only: q of each prompt's last token only, at row b (the last layer's queries)
   const int h_first = last_only && p != len - 1 ? NH : 0;
   const int nheads = NH + 2 * NKV;
-  // lane l holds dims 2l and 2l + 1 (4-byte accesses); its rotate-half partner is lane l ^ 32.
-  // The token's cos/sin row and both norm weights are loaded once; then per batch of QKV_HPB
-  // heads every raw head is requested before the first is used (one memory latency per batch).
-  const int d = 2 * lane;
-  const size_t cb = (size_t)p * HD + d;
-  const unsigned cw = *(const unsigned*)(cos_t + cb), sw = *(const unsigned*)(sin_t + cb);
-  const unsigned wq = *(const unsigned*)(qn + d), wk = *(const unsigned*)(kn + d);
-  const bf16* row = qkv + (size_t)t * nheads * HD + d;
-  for (int h0 = h_first + wave; h0 < nheads; h0 += 4 * QKV_HPB) {
-    unsigned xw[QKV_HPB];
+  const int d0 = 4 * j, d1 = 64 + 4 * j;
+  const size_t cb = (size_t)p * HD;
+  const u32x2 c0 = *(const u32x2*)(cos_t + cb + d0), c1 = *(const u32x2*)(cos_t + cb + d1);
+  const u32x2 s0 = *(const u32x2*)(sin_t + cb + d0), s1 = *(const u32x2*)(sin_t + cb + d1);
+  const u32x2 q0 = *(const u32x2*)(qn + d0), q1 = *(const u32x2*)(qn + d1);
+  const u32x2 k0 = *(const u32x2*)(kn + d0), k1 = *(const u32x2*)(kn + d1);
+  const float cw[8] = {lo_bf(c0.x), hi_bf(c0.x), lo_bf(c0.y), hi_bf(c0.y),
+                       lo_bf(c1.x), hi_bf(c1.x), lo_bf(c1.y), hi_bf(c1.y)};
+  const float sw[8] = {lo_bf(s0.x), hi_bf(s0.x), lo_bf(s0.y), hi_bf(s0.y),
+                       lo_bf(s1.x), hi_bf(s1.x), lo_bf(s1.y), hi_bf(s1.y)};
+  const bf16* row = qkv + (size_t)t * nheads * HD;
+  for (int h0 = h_first; h0 < nheads; h0 += QKV_HPB) {
+    u32x2 xa[QKV_HPB], xb[QKV_HPB];
 #pragma unroll
     for (int i = 0; i < QKV_HPB; ++i) {
-      const int h = h0 + 4 * i;
-      xw[i] = h < nheads ? *(const unsigned*)(row + (size_t)h * HD) : 0u;
+      const int h = h0 + i;
+      xa[i] = h < nheads ? *(const u32x2*)(row + (size_t)h * HD + d0) : u32x2{0u, 0u};
+      xb[i] = h < nheads ? *(const u32x2*)(row + (size_t)h * HD + d1) : u32x2{0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < QKV_HPB; ++i) {
-      const int h = h0 + 4 * i;
+      const int h = h0 + i;
       if (h >= nheads) break;
       if (h >= NH + NKV) {             // v: a straight copy into the cache
-        *(unsigned*)(vc + (((size_t)b * NKV + (h - NH - NKV)) * cap + p) * HD + d) = xw[i];
+        bf16* dst = vc + (((size_t)b * NKV + (h - NH - NKV)) * cap + p) * HD;
+        *(u32x2*)(dst + d0) = xa[i];
+        *(u32x2*)(dst + d1) = xb[i];
         continue;
       }
-      const unsigned ww = h < NH ? wq : wk;
-      const float x0 = lo_bf(xw[i]), x1 = hi_bf(xw[i]);
-      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const u32x2 wa = h < NH ? q0 : k0, wb = h < NH ? q1 : k1;
+      const float w[8] = {lo_bf(wa.x), hi_bf(wa.x), lo_bf(wa.y), hi_bf(wa.y),
+                          lo_bf(wb.x), hi_bf(wb.x), lo_bf(wb.y), hi_bf(wb.y)};
+      const float x[8] = {lo_bf(xa[i].x), hi_bf(xa[i].x), lo_bf(xa[i].y), hi_bf(xa[i].y),
+                          lo_bf(xb[i].x), hi_bf(xb[i].x), lo_bf(xb[i].y), hi_bf(xb[i].y)};
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss += x[k] * x[k];
+      ss = group16_sum(ss);
       const float r = rsqrt_ieee(ss / (float)HD + eps);
-      const float n0 = rbf(rbf(x0 * r) * lo_bf(ww));
-      const float n1 = rbf(rbf(x1 * r) * hi_bf(ww));
-      const float pn0 = __shfl_xor(n0, 32, 64), pn1 = __shfl_xor(n1, 32, 64);
+      float n[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) n[k] = rbf(rbf(x[k] * r) * w[k]);
       // first half: n cos - n[d + 64] sin; second half: n cos + n[d - 64] sin
-      const float sg = lane < 32 ? -1.0f : 1.0f;
-      const float o0 = rbf(n0 * lo_bf(cw)) + rbf(sg * pn0 * lo_bf(sw));
-      const float o1 = rbf(n1 * hi_bf(cw)) + rbf(sg * pn1 * hi_bf(sw));
+      float o[8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        o[k] = rbf(n[k] * cw[k]) + rbf(-n[k + 4] * sw[k]);
+        o[k + 4] = rbf(n[k + 4] * cw[k + 4]) + rbf(n[k] * sw[k + 4]);
+      }
       bf16* dst = h < NH ? q_out + ((size_t)(last_only ? b : t) * NH + h) * HD
                          : kc + (((size_t)b * NKV + (h - NH)) * cap + p) * HD;
-      *(unsigned*)(dst + d) = pk_bf16(o0, o1);
+      *(u32x2*)(dst + d0) = u32x2{pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
+      *(u32x2*)(dst + d1) = u32x2{pk_bf16(o[4], o[5]), pk_bf16(o[6], o[7])};
     }
   }
 }
@@ -342,9 +373,9 @@ DD_API int dd_qkv_post_prefill(const void* qkv, const void* qn, const void* kn, 
   DD_REQUIRE(HD == 128 && B >= 1 && T >= 1 && NKV >= 1 && NH >= NKV && NH % NKV == 0);
   DD_REQUIRE(cap >= 1 && rope_rows >= 1);
   DD_REQUIRE((long long)T * (NH + 2 * NKV) * HD < (1ll << 40));
-  hipLaunchKernelGGL(pf::qkv_prefill_kernel, dim3(T), dim3(256), 0, stream,
-                     (const bf16*)qkv, (const bf16*)qn, (const bf16*)kn, (const bf16*)cos_t,
-                     (const bf16*)sin_t, seq_start, B, last_only, (bf16*)q_out, (bf16*)kc,
+  hipLaunchKernelGGL(pf::qkv_prefill_kernel, dim3((T + pf::QKV_TPW - 1) / pf::QKV_TPW), dim3(256), 0,
+                     stream, (const bf16*)qkv, (const bf16*)qn, (const bf16*)kn, (const bf16*)cos_t,
+                     (const bf16*)sin_t, seq_start, B, T, last_only, (bf16*)q_out, (bf16*)kc,
                      (bf16*)vc, NH, NKV, cap, rope_rows, eps, err);
   return launch_status();
 }
