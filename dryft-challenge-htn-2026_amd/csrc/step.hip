@@ -139,17 +139,29 @@ constexpr int TMAX = 8;
 // The cross-wave reduction of a pass takes RED_TILES tile partials per round. The tiled layout
 // is the decode step's: a pass reads its tiles' rows at every k-step of the chunk.
 #ifndef DD_V_TS_GU
-#define DD_V_TS_GU 6                          // 80-row gate/up: tiles per pass
+#define DD_V_TS_GU 6                          // 80-row gate/up: tiles per pass (paired layout)
+#endif
+// 80-row gate/up in the decode step's chunk layout (1): one pass over the chunk's 5 row tiles
+// (its nf gate rows, then its nf up rows), reduced in rounds into one buffer of all 80 rows, the
+// SiLU epilogue once after the last round. (0: passes of DD_V_TS_GU tiles pairing 16-feature
+// gate and up tiles, so every reduction round ends with its own SiLU epilogue; 6 tiles = 48
+// feature slots for the chunk's 40, a sixth of the MFMAs and tile partials on empty rows.)
+#ifndef DD_V_GU_FLAT
+#define DD_V_GU_FLAT 1
 #endif
 #ifndef DD_V_TS_LM
 #define DD_V_TS_LM 4                          // 80-row lm_head: tiles per pass
 #endif
 template <int NM> struct MatCfg {
   static constexpr int TS(int k) {
-    return NM == 1 ? mat_T(k) : k == M_GU ? DD_V_TS_GU : k == M_LM ? DD_V_TS_LM : (mat_T(k) < 2 ? mat_T(k) : 2);
+    return NM == 1 ? mat_T(k)
+         : k == M_GU ? (DD_V_GU_FLAT ? mat_T(M_GU) : DD_V_TS_GU)
+         : k == M_LM ? DD_V_TS_LM : (mat_T(k) < 2 ? mat_T(k) : 2);
   }
   static constexpr int NSUB(int k) {
-    return NM == 1 ? 1 : k == M_GU ? (mat_CAPU(M_GU) + 8 * TS(k) - 1) / (8 * TS(k)) : mat_T(k) / TS(k);
+    return NM == 1 ? 1
+         : k == M_GU && !DD_V_GU_FLAT ? (mat_CAPU(M_GU) + 8 * TS(k) - 1) / (8 * TS(k))
+         : mat_T(k) / TS(k);
   }
   static constexpr int KB(int k) { return NM == 1 ? mat_KB1(k) : (k == M_O || k == M_D) ? DD_V_KBOD : DD_V_KB; }
   static constexpr int NBUF(int k) {
@@ -571,7 +583,7 @@ struct XOff {
 template <int KIND, int NM>
 __device__ __forceinline__ int pass_row(int rows, int sp, int t, int l16) {
   constexpr int TS = MatCfg<NM>::TS(KIND);
-  if (NM > 1 && KIND == M_GU) {             // tiles 0 .. TS/2 - 1 gate rows, then their up rows
+  if (NM > 1 && KIND == M_GU && !DD_V_GU_FLAT) {   // tiles 0 .. TS/2 - 1 gate rows, then their up rows
     constexpr int th = TS / 2;
     const int nf = rows >> 1, f = 16 * (th * sp + (t < th ? t : t - th)) + l16;
     return f < nf ? (t < th ? f : nf + f) : -1;
@@ -726,39 +738,51 @@ __device__ __forceinline__ void chunk_end(const Args& a, Shared& sh, const Geo& 
                                           f32x4 (&acc)[MatCfg<NM>::TS(KIND)][NM], int oslot,
                                           const unsigned (&hin)[NM]) {
   constexpr int TS = MatCfg<NM>::TS(KIND), CAPU = mat_CAPU(KIND), MS = 16 * NM, RW = MS + 1;
-  // RT tiles per reduction round (all NM activation tiles of each), NR rounds; gate/up rounds
-  // (NM > 1) pair gate tile r with its up tile r + TS / 2
-  constexpr int RT = TS * NM <= RED_TILES ? TS : RED_TILES / NM, NR = TS / RT;
-  static_assert(TS % RT == 0 && RT * NM <= RED_TILES && RT * 16 * RW <= RES_FLOATS, "reduction rounds");
+  // RT tiles per reduction round (all NM activation tiles of each), NR rounds. Paired gate/up
+  // rounds (NM > 1, DD_V_GU_FLAT 0) pair gate tile r with its up tile r + TS / 2 and run the
+  // epilogue per round; flat gate/up (FLAT) reduces every round into one buffer of all the
+  // chunk's rows (the LDS staging area, unused by 80-row steps) and runs the epilogue once.
+  constexpr bool FLAT = NM > 1 && KIND == M_GU && DD_V_GU_FLAT;
+  constexpr int RT = TS * NM <= RED_TILES ? TS : RED_TILES / NM;
+  constexpr int NR = FLAT ? (TS + RT - 1) / RT : TS / RT;
+  static_assert((FLAT || TS % RT == 0) && RT * NM <= RED_TILES && RT * 16 * RW <= RES_FLOATS, "reduction rounds");
+  static_assert(!FLAT || TS * 16 * RW * 4 <= (int)sizeof(sh.u.g.lgs), "flat gate/up rows fit the staging area");
   static_assert(NR == 1 || NM > 1, "several reduction rounds only in the 80-row instantiation");
   static_assert(NR == 1 || EPI == EPI_SILU || EPI == EPI_LOGITS, "several rounds: gate/up, lm_head");
   const int lane = tid() & 63, wave = wave_id();
   const int M = a.M;
   const int rows = chunk_rows<KIND>(g, ch);
   const int ua = g.u0 + ch * CAPU;            // first unit of the chunk
+  float* resb = FLAT ? (float*)&sh.u.g.lgs[0][0] : sh.u.g.res;
   STEP_TRACE(a.phase_cur, 7);
   STEP_TRACE_WAVE(a.phase_cur, 12);          // this wave's last batch of the chunk consumed
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
+    constexpr int RT0 = RT;
+    const int ntr = FLAT ? min(RT0, TS - r * RT0) : RT0;   // tiles of this round (compile-time)
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-      const int tt = EPI == EPI_SILU && NR > 1 ? (i == 0 ? r : r + TS / 2) : r * RT + i;
+      const int tt = EPI == EPI_SILU && NR > 1 && !FLAT ? (i == 0 ? r : r + TS / 2) : r * RT + i;
+      if (tt < TS) {
 #pragma unroll
-      for (int n = 0; n < NM; ++n) {
-        *(f32x4*)&sh.u.g.red[wave][i * NM + n][lane * 4] = acc[tt][n];
-        acc[tt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NM; ++n) {
+          *(f32x4*)&sh.u.g.red[wave][i * NM + n][lane * 4] = acc[tt][n];
+          acc[tt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
     lds_barrier();
-    // res[row j][m]: j = i * 16 + (lane / 16) * 4 + q of the D layout, m = 16 n + lane % 16
-    for (int e = tid(); e < RT * NM * 256; e += NTHR) {
+    // res[row j][m]: j = i * 16 + (lane / 16) * 4 + q of the D layout (FLAT: the chunk row, the
+    // round's first tile r RT), m = 16 n + lane % 16
+    const int jb = FLAT ? 16 * r * RT : 0;
+    for (int e = tid(); e < ntr * NM * 256; e += NTHR) {
       const int tn = e >> 8, ln = (e >> 2) & 63, q = e & 3;
       const int i = tn / NM, n = tn - i * NM;
       const float s = lds_sum8(&sh.u.g.red[0][tn][e & 255], RED_TILES * 256);
-      sh.u.g.res[(i * 16 + (ln >> 4) * 4 + q) * RW + 16 * n + (ln & 15)] = s;
+      resb[(jb + i * 16 + (ln >> 4) * 4 + q) * RW + 16 * n + (ln & 15)] = s;
     }
     lds_barrier();
-    chunk_epilogue<KIND, NM, EPI, STAGE>(a, sh, g, ch, sp, r, rows, ua, oslot, hin);
+    if (!FLAT || r == NR - 1) chunk_epilogue<KIND, NM, EPI, STAGE>(a, sh, g, ch, sp, r, rows, ua, oslot, hin);
   }
   STEP_TRACE(a.phase_cur, 8);
 }
@@ -806,17 +830,20 @@ __device__ __forceinline__ void chunk_epilogue(const Args& a, Shared& sh, const 
       }
     }
   } else if (EPI == EPI_SILU) {
-    // NM = 1: chunk rows 0 .. nf: gate features ua.., rows nf .. 2 nf: the matching up rows.
-    // NM > 1: round rows 0 .. 16: gate features ua + f0.., rows 16 .. 32: their up rows.
+    // NM = 1 and flat 80-row gate/up: chunk rows 0 .. nf: gate features ua.., rows nf .. 2 nf:
+    // the matching up rows. Paired 80-row passes: round rows 0 .. 16: gate features ua + f0..,
+    // rows 16 .. 32: their up rows.
+    constexpr bool FLAT = NM > 1 && DD_V_GU_FLAT;
+    const float* resb = FLAT ? (const float*)&sh.u.g.lgs[0][0] : sh.u.g.res;
     const int nfc = rows >> 1;
-    const int f0 = NM == 1 ? 0 : 16 * (TS / 2 * sp + r);
-    const int nf = NM == 1 ? nfc : min(16, nfc - f0);
-    const int up = NM == 1 ? nfc : 16;
+    const int f0 = NM == 1 || FLAT ? 0 : 16 * (TS / 2 * sp + r);
+    const int nf = NM == 1 || FLAT ? nfc : min(16, nfc - f0);
+    const int up = NM == 1 || FLAT ? nfc : 16;
     const rsrc_t mr = make_rsrc(m_slot(a, oslot), (unsigned)((size_t)M * a.I * 2));
     for (int e = t; e < nf * M; e += NTHR) {
       const int m = e / nf, f = e - m * nf;
-      const float gv = rbf(sh.u.g.res[f * RW + m]);
-      const float uv = rbf(sh.u.g.res[(up + f) * RW + m]);
+      const float gv = rbf(resb[f * RW + m]);
+      const float uv = rbf(resb[(up + f) * RW + m]);
       const float sl = rbf(gv / (1.0f + expf(-gv)));
       if (STAGE) sh.u.g.lgs[m][ch * CAPU + f0 + f] = f2bf(sl * uv);
       else stc_b16(mr, xoff(m, ua + f0 + f, M) * 2, f2bf(sl * uv));
