@@ -1755,6 +1755,62 @@ __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool f
 // Combine the (o, m, l) partials of a (sequence, kv head) split over attention workgroups
 // fw .. lw (in workgroup order) into the bf16 attention output; run by the last contributor to
 // arrive. Pair start S: a contributor's record is its slot 0 when the pair is its first segment.
+// The combine with two query tiles (R = W G rows, 20 at W = 5). Merging element by element
+// (a thread's 5 elements, each with its own round of loads) kept the combining workgroup 3.2-3.8
+// us past its arrival. Here thread t takes 8 consecutive dims of one row (R x 16 threads): per
+// contributor two 16-byte loads of o and one of (m, l), all ATT_CB contributors' loads in flight
+// together, the merge in registers in contributor order (the same operations on the same values
+// as the per-element merge), and one 16-byte store of the 8 outputs.
+#ifndef DD_ATT_CMB_1R
+#define DD_ATT_CMB_1R 1
+#endif
+__device__ __forceinline__ void attn_combine_1r(const Args& a, const Shared& sh, int layer, int b,
+                                                int kvh, int S, int fw, int lw, int P, int gx) {
+  constexpr int DPT = 8, TPR = HD / DPT;                  // dims per thread, threads per row
+  const int NH = a.NH, G = a.NH / a.NKV, R = att_rows(a);
+  const int t = tid();
+  if (t >= R * TPR) return;
+  const int row = t / TPR, d0 = (t - row * TPR) * DPT;
+  const int ovt = sh.aovh - att_ovh_head(sh.aovh);
+  const rsrc_t pr = make_rsrc(att_part(a, layer), (unsigned)((size_t)gridDim.x * 2 * R * ATT_REC * 4));
+  const rsrc_t orr = make_rsrc(attn_slot(a, layer), (unsigned)((size_t)a.M * NH * HD * 2));
+  float Mx = -INFINITY, l = 0.f, o[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) o[i] = 0.f;
+  for (int c0 = fw; c0 <= lw; c0 += ATT_CB) {
+    u32x4 oa[ATT_CB], ob[ATT_CB], ml[ATT_CB];
+#pragma unroll
+    for (int j = 0; j < ATT_CB; ++j) {
+      const int c = c0 + j;
+      const bool ok = c <= lw && sh.afirst[c + 1] > sh.afirst[c];
+      const unsigned ro =
+          (unsigned)((((c * P + gx) * 2 + (sh.afirst[c] >= S - ovt ? 0 : 1)) * R + row) * ATT_REC) * 4;
+      oa[j] = ldc_b128(pr, ok ? ro + d0 * 4 : OOB);
+      ob[j] = ldc_b128(pr, ok ? ro + (d0 + 4) * 4 : OOB);
+      ml[j] = ok ? ldc_b128(pr, ro + HD * 4) : u32x4{0xff800000u, 0u, 0u, 0u};   // m = -inf: skipped
+    }
+#pragma unroll
+    for (int j = 0; j < ATT_CB; ++j) {
+      const float mv = __uint_as_float(ml[j].x), lv = __uint_as_float(ml[j].y);
+      if (mv == -INFINITY) continue;
+      const float Mn = fmaxf(Mx, mv);
+      const float fo = exp2_hw(Mx - Mn), fn = exp2_hw(mv - Mn);
+      const float ov[DPT] = {__uint_as_float(oa[j].x), __uint_as_float(oa[j].y), __uint_as_float(oa[j].z),
+                             __uint_as_float(oa[j].w), __uint_as_float(ob[j].x), __uint_as_float(ob[j].y),
+                             __uint_as_float(ob[j].z), __uint_as_float(ob[j].w)};
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) o[i] = o[i] * fo + ov[i] * fn;
+      l = l * fo + lv * fn;
+      Mx = Mn;
+    }
+  }
+  const float inv = 1.0f / l;
+  const int s = row / G, g = row - s * G;
+  stc_b128(orr, xoff(b * a.W + s, (kvh * G + g) * HD + d0, a.M) * 2,
+           u32x4{pk_bf16(o[0] * inv, o[1] * inv), pk_bf16(o[2] * inv, o[3] * inv),
+                 pk_bf16(o[4] * inv, o[5] * inv), pk_bf16(o[6] * inv, o[7] * inv)});
+}
+
 __device__ __forceinline__ void attn_combine(const Args& a, const Shared& sh, int layer, int b,
                                              int kvh, int S, int fw, int lw, int P, int gx) {
   const int NH = a.NH, G = a.NH / a.NKV, R = att_rows(a);
@@ -2309,7 +2365,10 @@ __device__ __forceinline__ void attention_phase(const Args& a, Shared& sh, int l
         }
         __syncthreads();
         if (sg == 0) STEP_TRACE(p, 8);          // arrival counted
-        if (sh.flag) attn_combine(a, sh, layer, b, kvh, S, fw, lw, P, gx);
+        if (sh.flag) {
+          if (DD_ATT_CMB_1R && NQT > 1) attn_combine_1r(a, sh, layer, b, kvh, S, fw, lw, P, gx);
+          else attn_combine(a, sh, layer, b, kvh, S, fw, lw, P, gx);
+        }
         if (sg == 0) STEP_TRACE(p, 10);
       }
       __syncthreads();
