@@ -1607,10 +1607,11 @@ __device__ __forceinline__ void head_norm_rope(const Args& a, float& x0, float& 
 // The units are split over the first Ga workgroups, Ga = min(grid, T / ATT_MINU): a small
 // workload (short contexts, B = 1) stays on fewer workgroups, at least ATT_MINU units each
 // (measured at B = 1: 8 is 2.3% faster per step than 16; with the split overhead units 6 is 0.6%
-// faster than 8 and 12 is 2% slower; B = 16 is the same for 6-12). Partition arithmetic stays in
-// 32 bits (units x workgroups < 2^31, checked on the host).
+// faster than 8 and 12 is 2% slower; later 4 is 0.7% faster than 6, 3 and 5 in between; B = 16
+// and the verify step are the same for 4-12). Partition arithmetic stays in 32 bits (units x
+// workgroups < 2^31, checked on the host).
 #ifndef DD_ATT_MINU
-#define DD_ATT_MINU 6
+#define DD_ATT_MINU 4
 #endif
 constexpr int ATT_MINU = DD_ATT_MINU;
 __device__ __forceinline__ int attn_owner(int T, int Ga, int i) {  // workgroup of global unit i
@@ -1624,11 +1625,12 @@ __device__ __forceinline__ int attn_first(int T, int Ga, int c) {  // first unit
 // (prologue, wave merge, output) followed by one unit per 32-key block, so a workgroup holding
 // many short segments gets fewer blocks. With one or two sequences the few pairs are spread over
 // more workgroups by a larger weight (B = 16 best at 12; at B = 1 any weight from 8 to 48
-// measures the same with ATT_MINU 8). A verify-shaped segment (W G query rows: prologue and
+// measured the same with ATT_MINU 8; with ATT_MINU 4, 48 is 0.1% faster than 24 and 12 0.2%
+// slower). A verify-shaped segment (W G query rows: prologue and
 // merge of two query tiles) weighs more: 36 (B = 16, W = 5: 6.48 -> 6.19 ms per step; 48 and
 // 64 measured 6.27 and 6.35).
 #ifndef DD_ATT_OVH_SMALL
-#define DD_ATT_OVH_SMALL 24
+#define DD_ATT_OVH_SMALL 48
 #endif
 #ifndef DD_ATT_OVH
 #define DD_ATT_OVH 12
