@@ -24,6 +24,8 @@
 // O^T += V^T.P^T; the key order inside each P.V contraction is the one each lane's S^T
 // accumulators hold, so P never leaves the lane. A wave skips the blocks past its last token.
 // Tiles holding a prompt's last tokens (the longest causal prefixes) are scheduled first.
+#include <type_traits>
+
 #include "common.h"
 
 namespace dd {
@@ -264,8 +266,10 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
       vst[r] = *(const u32x4*)(vc + kvbase + (size_t)key * HD + vdg * 8);
     }
   };
-  fetch(0);
-  for (int blk = 0; blk < nblk; ++blk) {
+  // One block: stage it, request the next, then (the wave's keys permitting) add it. MASKED: the
+  // causal mask key <= query position; blocks wholly before the tile's first query need none.
+  auto block = [&](int blk, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
     const int key0 = blk * KB;
     __syncthreads();                                          // the previous block is consumed
 #pragma unroll
@@ -284,7 +288,7 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
     }
     __syncthreads();
     if (blk + 1 < nblk) fetch(key0 + KB);                     // in flight during this block
-    if (!wact || key0 > wlast) continue;                      // wave-uniform: nothing to add
+    if (!wact || key0 > wlast) return;                        // wave-uniform: nothing to add
     // S^T = K.Q^T: two 16-key halves; D layout: key = t * 16 + g4 * 4 + i, query column l16
     u32x4 ka[2][4];
 #pragma unroll
@@ -308,7 +312,7 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = key0 + t * 16 + g4 * 4 + i;
-          const float v = qok && key <= pq ? sc[t][i] * scale_log2 : -INFINITY;
+          const float v = !MASKED || (qok && key <= pq) ? sc[t][i] * scale_log2 : -INFINITY;
           sv[t * 4 + i] = v;
           mloc = fmaxf(mloc, v);
         }
@@ -342,7 +346,13 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
         acc[h][dt] = mfma16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pB, acc[h][dt]);
       }
     }
-  }
+  };
+  // blocks whose last key is at or before the workgroup's first query position: no mask; then the
+  // blocks that reach into the tile
+  const int nfull = min(nblk, (p0 + 1) / KB);
+  fetch(0);
+  for (int blk = 0; blk < nfull; ++blk) block(blk, std::integral_constant<bool, false>{});
+  for (int blk = nfull; blk < nblk; ++blk) block(blk, std::integral_constant<bool, true>{});
   // out: O^T D layout: dim dt * 16 + g4 * 4 + i, token column l16
   if (!qok) return;
 #pragma unroll
