@@ -17,9 +17,10 @@
 // flash_prefill_kernel: one workgroup of 4 waves per (tile of 16 NTT tokens of one prompt, kv
 // head). Wave w takes token tile w / (G / HPW) and HPW of the kv head's G query heads, so each K
 // and V^T fragment a wave reads from LDS feeds HPW query tiles; the 4 waves stage every 32-key
-// block (K row-major, V transposed) into LDS once for the whole tile, the next block's global
-// loads in flight during the current block. Per block: S^T = K.Q^T on MFMA 16x16x32 (A = 16 keys
-// x 32 dims from LDS, B = Q^T held in registers), causal mask key <= token position, online
+// block (K and V row-major, V^T read by transposing LDS loads) into LDS once for the whole tile,
+// the next block's global loads in flight during the current block. Per block: S^T = K.Q^T on
+// MFMA 16x16x32 (A = 16 keys x 32 dims from LDS, B = Q^T held in registers), causal mask key <=
+// token position (only on the blocks that reach into the tile), online
 // softmax in the log2 domain (scale HD^-0.5 log2 e), P rounded to bf16 (fused.py:335),
 // O^T += V^T.P^T; the key order inside each P.V contraction is the one each lane's S^T
 // accumulators hold, so P never leaves the lane. A wave skips the blocks past its last token.
@@ -36,21 +37,29 @@ constexpr int HALF = 64;
 constexpr int NWAVE_F = 4;             // waves per flash workgroup
 constexpr int KB = 32;                 // keys per block
 constexpr int MAXG = 8;                // query heads per kv head
-constexpr int KROW = HD + 8;           // LDS K row (elements): 272 bytes
-constexpr int VROW = KB + 4;           // LDS V^T row (elements): 72 bytes (18 words: the 4
-                                       // dim rows one staging store spans fall in 4 disjoint
-                                       // 16-bank ranges)
+constexpr int KROW = HD + 8;           // LDS K / V row (elements): 272 bytes
 
-// The value of lane l ^ 16 (l ^ 32) through gfx950's v_permlane16_swap (v_permlane32_swap), a
-// VALU operation, instead of the LDS round trip (ds_bpermute) __shfl_xor compiles to: swapping a
-// register with itself leaves each lane the pair (value of the lower row, value of the upper row).
-__device__ __forceinline__ float lane_xor16(float v) {
+// Max and sum over the lane pairs l, l ^ 16 (rows16) and l, l ^ 32 (rows32) through gfx950's
+// v_permlane16_swap / v_permlane32_swap, VALU operations, instead of the LDS round trip
+// (ds_bpermute) __shfl_xor compiles to. Swapping a register with itself leaves the pair (value of
+// the lower row, value of the upper row) in every lane, so the pair's max or sum needs no
+// lane-dependent select; the sum adds the lower row's value first in every lane, the same bits as
+// either order.
+__device__ __forceinline__ float max_rows16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float lane_xor32(float v) {
+__device__ __forceinline__ float max_rows32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_rows16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_rows32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // prompt and position of packed token t (seq_start: B + 1 ascending offsets)
@@ -161,8 +170,18 @@ qkv_prefill_kernel(const bf16* __restrict__ qkv, const bf16* __restrict__ qn,
 
 struct FlashShared {
   bf16 k[KB][KROW];                    // the block's keys, row-major
-  bf16 vt[HD][VROW];                   // the block's values, transposed: [dim][key]
+  bf16 v[KB][KROW];                    // the block's values, row-major (read transposed)
 };
+
+// ds_read_b64_tr_b16 (gfx950), a transposing LDS read: when lane (l16, g4) of a wave addresses
+// row g4 * 4 + l16 / 4, columns c0 + 4 (l16 % 4) .. + 3 of a row-major bf16 array, it receives
+// column c0 + l16 of rows g4 * 4 .. g4 * 4 + 3 (the MFMA operand of the transposed block).
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(const bf16* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(const_cast<bf16*>(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
 
 // Tile index -> (prompt, first token position) for tiles of TQ tokens. ntile[b] = ceil(len_b /
 // TQ); tiles are numbered prompt by prompt, and workgroup x takes tile (total - 1 - x), so the
@@ -246,26 +265,30 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
     for (int dt = 0; dt < 8; ++dt) acc[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const size_t kvbase = ((size_t)b * NKV + kvh) * cap * HD;
-  // staging per block: K as 512 16-byte chunks (2 a thread: key c / 16, dims (c % 16) 8 ..);
-  // V as 256 pairs of 16-byte chunks (one a thread: keys 2 kp and 2 kp + 1 at dims dg 8 ..,
-  // kp = t % 16, dg = t / 16), stored transposed as 4-byte words holding both keys of one dim
+  // staging per block: K and V as 512 16-byte chunks each, 2 of each a thread (chunk c: key
+  // c / 16, dims (c % 16) 8 ..), both stored row-major. Buffer loads over this (sequence, kv
+  // head)'s cache rows: the per-lane offsets are fixed and the block's key0 goes in the scalar
+  // offset; keys past the cache read zeros (they are masked).
   constexpr int CPT = KB * HD / 8 / (64 * NWAVE_F);
-  static_assert(KB * HD / 16 == 64 * NWAVE_F, "one V chunk pair per thread");
-  u32x4 kst[CPT], vst[2];
-  const int vkp = (int)threadIdx.x & 15, vdg = (int)threadIdx.x >> 4;
+  static_assert(CPT * 64 * NWAVE_F * 8 == KB * HD, "whole chunks per thread");
+  const rsrc_t kr = make_rsrc(kc + kvbase, (unsigned)((size_t)cap * HD * 2));
+  const rsrc_t vr = make_rsrc(vc + kvbase, (unsigned)((size_t)cap * HD * 2));
+  unsigned coff[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = (int)threadIdx.x + i * 64 * NWAVE_F;
+    coff[i] = (unsigned)((c >> 4) * HD * 2 + (c & 15) * 16);
+  }
+  u32x4 kst[CPT], vst[CPT];
   auto fetch = [&](int key0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = (int)threadIdx.x + i * 64 * NWAVE_F;
-      const int key = min(key0 + (c >> 4), cap - 1);
-      kst[i] = *(const u32x4*)(kc + kvbase + (size_t)key * HD + (c & 15) * 8);
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int key = min(key0 + 2 * vkp + r, cap - 1);
-      vst[r] = *(const u32x4*)(vc + kvbase + (size_t)key * HD + vdg * 8);
+      kst[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, coff[i], (unsigned)key0 * HD * 2, 0);
+      vst[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, coff[i], (unsigned)key0 * HD * 2, 0);
     }
   };
+  // V^T operand addressing (see lds_read_tr16)
+  const int trow = g4 * 4 + (l16 >> 2), tcol = 4 * (l16 & 3);
   // One block: stage it, request the next, then (the wave's keys permitting) add it. MASKED: the
   // causal mask key <= query position; blocks wholly before the tile's first query need none.
   auto block = [&](int blk, auto masked) {
@@ -276,15 +299,7 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
     for (int i = 0; i < CPT; ++i) {
       const int c = (int)threadIdx.x + i * 64 * NWAVE_F;
       *(u32x4*)&sh.k[c >> 4][(c & 15) * 8] = kst[i];
-    }
-    {
-      const unsigned w0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};   // key 2 kp
-      const unsigned w1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};   // key 2 kp + 1
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *(unsigned*)&sh.vt[vdg * 8 + 2 * j][2 * vkp] = (w0[j] & 0xffffu) | (w1[j] << 16);
-        *(unsigned*)&sh.vt[vdg * 8 + 2 * j + 1][2 * vkp] = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
-      }
+      *(u32x4*)&sh.v[c >> 4][(c & 15) * 8] = vst[i];
     }
     __syncthreads();
     if (blk + 1 < nblk) fetch(key0 + KB);                     // in flight during this block
@@ -316,8 +331,7 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
           sv[t * 4 + i] = v;
           mloc = fmaxf(mloc, v);
         }
-      mloc = fmaxf(mloc, lane_xor16(mloc));
-      mloc = fmaxf(mloc, lane_xor32(mloc));
+      mloc = max_rows32(max_rows16(mloc));
       const float m_new = fmaxf(m_run[h], mloc);
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = exp2_hw(m_run[h] - msafe);
@@ -330,8 +344,7 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
         psum += pa + pb;
         pk[jj] = pk_bf16(pa, pb);
       }
-      psum += lane_xor16(psum);
-      psum += lane_xor32(psum);
+      psum = sum_rows32(sum_rows16(psum));
       l_run[h] = l_run[h] * alpha + psum;
       m_run[h] = m_new;
       const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
@@ -339,9 +352,8 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
       // 16 + g4 * 4 .. + 3 (the keys the lane's P values belong to)
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int d = dt * 16 + l16;
-        const u32x2 lo = *(const u32x2*)&sh.vt[d][g4 * 4];
-        const u32x2 hi = *(const u32x2*)&sh.vt[d][16 + g4 * 4];
+        const u32x2 lo = lds_read_tr16(&sh.v[trow][dt * 16 + tcol]);
+        const u32x2 hi = lds_read_tr16(&sh.v[16 + trow][dt * 16 + tcol]);
         acc[h][dt] *= alpha;
         acc[h][dt] = mfma16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pB, acc[h][dt]);
       }
