@@ -538,7 +538,11 @@ def main():
               f"identical={same})", file=sys.stderr, flush=True)
 
     if not args.no_fp8:                       # opt-in fp8 prefill GEMMs (B <= 8)
-        p8 = prompts[:8]
+        # The fp8 GEMMs take a packed row count that is a multiple of 16 (the reference's
+        # _fp8_lin, engine.py:451-457, runs bf16 otherwise), so the last prompt is shortened by
+        # the remainder: both legs then time the same 16k-row batch.
+        p8 = [list(p) for p in prompts[:8]]
+        p8[-1] = p8[-1][:len(p8[-1]) - sum(len(p) for p in p8) % 16]
         ms_bf, n8 = run_prefill(torch, eng, p8)
         eng._quantize_fp8()
         eng.fp8 = True
