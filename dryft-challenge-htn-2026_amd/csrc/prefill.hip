@@ -34,7 +34,6 @@ namespace pf {
 
 constexpr int HD = 128;
 constexpr int HALF = 64;
-constexpr int NWAVE_F = 4;             // waves per flash workgroup
 constexpr int KB = 32;                 // keys per block
 constexpr int MAXG = 8;                // query heads per kv head
 constexpr int KROW = HD + 8;           // LDS K / V row (elements): 272 bytes
@@ -216,12 +215,15 @@ __device__ __forceinline__ bool tile_of(const int* __restrict__ seq_start, int B
 
 // q [T, NH, HD] token-major; out [T, NH * HD] (last_only: [B, NH, HD] / [B, NH * HD], row b =
 // prompt b's last token). HPW query heads per wave, NTT 16-token tiles per workgroup, with
-// NTT * (NH / NKV) / HPW = 4 waves.
+// NTT * (NH / NKV) / HPW = NWAVE_F waves; MINB workgroups per CU (the register budget).
+#ifndef DD_PF_MINB1
+#define DD_PF_MINB1 4
+#endif
 #ifndef DD_PF_MINB
 #define DD_PF_MINB 2
 #endif
-template <int HPW, int NTT>
-__global__ void __launch_bounds__(64 * NWAVE_F, DD_PF_MINB)
+template <int HPW, int NTT, int NWAVE_F, int MINB>
+__global__ void __launch_bounds__(64 * NWAVE_F, MINB)
 flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ vc,
                      const int* __restrict__ seq_start, int B, int T, bf16* __restrict__ out,
                      int NH, int NKV, int cap, int last_only, float scale_log2) {
@@ -414,23 +416,29 @@ DD_API int dd_attn_prefill(const void* q, const void* kc, const void* vc, const 
   // Python floats to a float32 kernel argument)
   const float scale_log2 = (float)(1.0 / sqrt((double)HD) * 1.4426950408889634);
   // 4 waves: HPW heads x (16 NTT tokens) per wave group; tiles per launch at most T / TQ + B
-  auto launch = [&](auto kern, int TQ) {
+  auto launch = [&](auto kern, int TQ, int nw) {
     const int ntiles = last_only ? B : T / TQ + B;
-    hipLaunchKernelGGL(kern, dim3(ntiles, NKV), dim3(64 * pf::NWAVE_F), 0, stream, (const bf16*)q,
+    hipLaunchKernelGGL(kern, dim3(ntiles, NKV), dim3(64 * nw), 0, stream, (const bf16*)q,
                        (const bf16*)kc, (const bf16*)vc, seq_start, B, T, (bf16*)out, NH, NKV, cap,
                        last_only, scale_log2);
   };
   switch (G) {
-    case 1: launch(pf::flash_prefill_kernel<1, 4>, 64); break;
-    case 2: launch(pf::flash_prefill_kernel<2, 4>, 64); break;
+    case 1: launch(pf::flash_prefill_kernel<1, 4, 4, DD_PF_MINB>, 64, 4); break;
+    case 2: launch(pf::flash_prefill_kernel<2, 4, 4, DD_PF_MINB>, 64, 4); break;
+// G = 4 (Qwen3): one query head per wave, 16 tokens per workgroup. At 108 VGPRs four such
+// workgroups share a CU (four waves per SIMD), against two of the two-heads-per-wave kernel
+// (211 VGPRs): configs[4]'s packed prompts, one process alternating builds, 368 -> 338 us per
+// layer, the same bits. Eight waves per workgroup (32 tokens, one head each, 96 VGPRs) measured
+// 370 us; five or six workgroups per CU spill (676 / 805 us).
 #ifndef DD_PF_G4
-#define DD_PF_G4 2
+#define DD_PF_G4 1
 #endif
     case 4:
-      if (DD_PF_G4 == 4) launch(pf::flash_prefill_kernel<4, 4>, 64);   // 4 heads x 16 tokens a wave
-      else launch(pf::flash_prefill_kernel<2, 2>, 32);                  // 2 heads x 16 tokens a wave
+      if (DD_PF_G4 == 4) launch(pf::flash_prefill_kernel<4, 4, 4, DD_PF_MINB>, 64, 4);
+      else if (DD_PF_G4 == 1) launch(pf::flash_prefill_kernel<1, 1, 4, DD_PF_MINB1>, 16, 4);
+      else launch(pf::flash_prefill_kernel<2, 2, 4, DD_PF_MINB>, 32, 4);
       break;
-    default: launch(pf::flash_prefill_kernel<2, 1>, 16); break;   // G = 8: 4 waves per token tile
+    default: launch(pf::flash_prefill_kernel<2, 1, 4, DD_PF_MINB>, 16, 4); break;   // G = 8
   }
   return launch_status();
 }
