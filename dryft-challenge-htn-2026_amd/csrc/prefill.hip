@@ -25,6 +25,8 @@
 // O^T += V^T.P^T; the key order inside each P.V contraction is the one each lane's S^T
 // accumulators hold, so P never leaves the lane. A wave skips the blocks past its last token.
 // Tiles holding a prompt's last tokens (the longest causal prefixes) are scheduled first.
+// flash_prefill_dma_kernel: the same arithmetic for G = 4 with one query head per wave, its
+// 32-key blocks staged by LDS-DMA loads into two swizzled LDS buffers (the G = 4 default).
 #include <type_traits>
 
 #include "common.h"
@@ -380,6 +382,156 @@ flash_prefill_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, co
   }
 }
 
+// The same attention (one query head per wave, 16 tokens, G = 4 waves per workgroup) with the
+// 32-key blocks staged by LDS-DMA loads (buffer_load_dwordx4 ... lds: lane i's 16 bytes land at
+// the wave's LDS base + 16 i) into two buffers: block j + 1 streams into one while block j is
+// read from the other, with one barrier per block and no staging registers. Rows are 256 bytes,
+// unpadded; 16-byte chunks are XOR-swizzled so that the MFMA operand reads meet distinct banks:
+// K chunk c of key r at position c ^ (r % 16) (a K read: 16 consecutive keys, one chunk), V chunk
+// c of key r at c ^ 2 (r % 8) (a transposing V read: 4 consecutive keys, a pair of chunks).
+// The DMA writer picks, per lane, the source chunk whose swizzled position is its own. The loop is
+// unrolled by two so each buffer is a separate LDS object at every access.
+struct FlashDmaBuf {
+  bf16 k[KB * HD];
+  bf16 v[KB * HD];
+};
+
+template <int MINB>
+__global__ void __launch_bounds__(256, MINB)
+flash_prefill_dma_kernel(const bf16* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ vc,
+                         const int* __restrict__ seq_start, int B, int T, bf16* __restrict__ out,
+                         int NH, int NKV, int cap, int last_only, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) FlashDmaBuf sb0;
+  __shared__ __attribute__((aligned(16))) FlashDmaBuf sb1;
+  constexpr int TQ = 16;
+  int b = 0, p0 = 0;
+  if (!tile_of(seq_start, B, blockIdx.x, last_only != 0, TQ, b, p0)) return;
+  const int G = NH / NKV, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int head = kvh * G + wave;                              // this wave's query head
+  const int s0 = seq_start[b], len = seq_start[b + 1] - s0;
+  if (s0 < 0 || len <= 0 || s0 + len > T || len > cap) return;   // inconsistent offsets: no access
+  const int pq = p0 + l16;                                      // this lane's query token position
+  const bool qok = last_only ? pq == len - 1 : pq < len;
+  const bool wact = last_only ? (len - 1 >= p0 && len - 1 < p0 + 16) : p0 < len;
+  const int wlast = min(p0 + 15, len - 1);
+  const int nblk = wlast / KB + 1;
+  u32x4 qreg[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    qreg[kb] = qok ? *(const u32x4*)(q + ((size_t)(last_only ? b : s0 + pq) * NH + head) * HD + kb * 32 + g4 * 8)
+                   : u32x4{0u, 0u, 0u, 0u};
+  f32x4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const size_t kvbase = ((size_t)b * NKV + kvh) * cap * HD;
+  const rsrc_t kr = make_rsrc(kc + kvbase, (unsigned)((size_t)cap * HD * 2));
+  const rsrc_t vr = make_rsrc(vc + kvbase, (unsigned)((size_t)cap * HD * 2));
+  // DMA: wave w writes LDS positions (2 w + j) 64 + lane (16-byte chunks) of each matrix
+  unsigned koff[2], voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = (2 * wave + j) * 64 + lane, r = p >> 4, c = p & 15;
+    koff[j] = (unsigned)(r * HD * 2 + ((c ^ (r & 15)) * 16));
+    voff[j] = (unsigned)(r * HD * 2 + ((c ^ (2 * (r & 7))) * 16));
+  }
+  typedef __attribute__((address_space(3))) void* lds_t;
+  auto issue = [&](FlashDmaBuf& s, int key0) {
+    const unsigned so = (unsigned)key0 * HD * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_t)&s.k[(2 * wave + j) * 512], 16, koff[j], so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_t)&s.v[(2 * wave + j) * 512], 16, voff[j], so, 0, 0);
+    }
+  };
+  // MFMA operand addresses (elements) inside a buffer
+  int ka_off[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int r = t * 16 + l16, c = kb * 4 + g4;
+      ka_off[t][kb] = r * HD + ((c ^ (r & 15)) << 3);
+    }
+  const int trow = g4 * 4 + (l16 >> 2), tcol = 4 * (l16 & 3);
+  int vt_off[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const int r = hh * 16 + trow, col = dt * 16 + tcol;
+      vt_off[hh][dt] = r * HD + ((((col >> 3) ^ (2 * (r & 7)))) << 3) + (col & 7);
+    }
+  const int nfull = min(nblk, (p0 + 1) / KB);                  // blocks that need no causal mask
+  // one block: wait for its DMA (this wave's, then every wave's through the barrier), start the
+  // next block's DMA into the other buffer (free: every wave is past its previous block), then
+  // (the wave's keys permitting) add it
+  auto block = [&](const FlashDmaBuf& cur, FlashDmaBuf& nxt, int blk) {
+    const int key0 = blk * KB;
+    __builtin_amdgcn_s_waitcnt(0x0f70);                        // vmcnt(0)
+    __syncthreads();
+    if (blk + 1 < nblk) issue(nxt, key0 + KB);
+    if (!wact || key0 > wlast) return;                          // wave-uniform: nothing to add
+    const bool masked = blk >= nfull;
+    f32x4 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) d = mfma16x16x32(*(const u32x4*)&cur.k[ka_off[t][kb]], qreg[kb], d);
+      sc[t] = d;
+    }
+    float sv[8];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + t * 16 + g4 * 4 + i;
+        const float v = !masked || (qok && key <= pq) ? sc[t][i] * scale_log2 : -INFINITY;
+        sv[t * 4 + i] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    mloc = max_rows32(max_rows16(mloc));
+    const float m_new = fmaxf(m_run, mloc);
+    const float msafe = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_hw(m_run - msafe);
+    float psum = 0.f;
+    unsigned pk[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float pa = exp2_hw(sv[2 * jj] - msafe);
+      const float pb = exp2_hw(sv[2 * jj + 1] - msafe);
+      psum += pa + pb;
+      pk[jj] = pk_bf16(pa, pb);
+    }
+    psum = sum_rows32(sum_rows16(psum));
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    const u32x4 pB = {pk[0], pk[1], pk[2], pk[3]};
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const u32x2 lo = lds_read_tr16(&cur.v[vt_off[0][dt]]);
+      const u32x2 hi = lds_read_tr16(&cur.v[vt_off[1][dt]]);
+      acc[dt] *= alpha;
+      acc[dt] = mfma16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pB, acc[dt]);
+    }
+  };
+  issue(sb0, 0);
+  for (int blk = 0; blk < nblk; blk += 2) {
+    block(sb0, sb1, blk);
+    if (blk + 1 < nblk) block(sb1, sb0, blk + 1);
+  }
+  if (!qok) return;
+  bf16* orow = last_only ? out + ((size_t)b * NH + head) * HD : out + ((size_t)(s0 + pq) * NH + head) * HD;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) orow[dt * 16 + g4 * 4 + i] = f2bf(acc[dt][i] / l_run);
+}
+
 }  // namespace pf
 }  // namespace dd
 
@@ -425,18 +577,21 @@ DD_API int dd_attn_prefill(const void* q, const void* kc, const void* vc, const 
   switch (G) {
     case 1: launch(pf::flash_prefill_kernel<1, 4, 4, DD_PF_MINB>, 64, 4); break;
     case 2: launch(pf::flash_prefill_kernel<2, 4, 4, DD_PF_MINB>, 64, 4); break;
-// G = 4 (Qwen3): one query head per wave, 16 tokens per workgroup. At 108 VGPRs four such
-// workgroups share a CU (four waves per SIMD), against two of the two-heads-per-wave kernel
-// (211 VGPRs): configs[4]'s packed prompts, one process alternating builds, 368 -> 338 us per
-// layer, the same bits. Eight waves per workgroup (32 tokens, one head each, 96 VGPRs) measured
-// 370 us; five or six workgroups per CU spill (676 / 805 us).
+// G = 4 (Qwen3): one query head per wave, 16 tokens per workgroup, four workgroups per CU (four
+// waves per SIMD). configs[4]'s packed prompts, one process alternating builds, us per layer, the
+// same bits throughout: two heads per wave (211 VGPRs, two workgroups per CU) 368; one head per
+// wave with register staging (108 VGPRs) 338; with the LDS-DMA double buffer (116 VGPRs, 32 KB
+// of LDS) 314-322 against 347-354 on the same boxes. Eight waves per workgroup (32 tokens) 370;
+// five or six workgroups per CU spill (349 with DMA; 676 / 805 without). The DMA kernel's last
+// block may reach past a prompt's keys but not past the cache: it needs cap % 32 == 0 (the
+// engine's capacities are multiples of 128), else the register-staged kernel runs.
 #ifndef DD_PF_G4
-#define DD_PF_G4 1
+#define DD_PF_G4 5
 #endif
     case 4:
-      if (DD_PF_G4 == 4) launch(pf::flash_prefill_kernel<4, 4, 4, DD_PF_MINB>, 64, 4);
-      else if (DD_PF_G4 == 1) launch(pf::flash_prefill_kernel<1, 1, 4, DD_PF_MINB1>, 16, 4);
-      else launch(pf::flash_prefill_kernel<2, 2, 4, DD_PF_MINB>, 32, 4);
+      if (DD_PF_G4 == 5 && cap % pf::KB == 0) launch(pf::flash_prefill_dma_kernel<DD_PF_MINB1>, 16, 4);
+      else if (DD_PF_G4 == 2) launch(pf::flash_prefill_kernel<2, 2, 4, DD_PF_MINB>, 32, 4);
+      else launch(pf::flash_prefill_kernel<1, 1, 4, DD_PF_MINB1>, 16, 4);
       break;
     default: launch(pf::flash_prefill_kernel<2, 1, 4, DD_PF_MINB>, 16, 4); break;   // G = 8
   }

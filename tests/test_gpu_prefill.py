@@ -170,6 +170,34 @@ def test_attn_prefill_packed(cuda, lens, NH, NKV, cap):
     print(f"lens={lens} G={NH // NKV}: max|out - fp64| {d:.3g}")
 
 
+def test_attn_prefill_dma_equals_register_staging(cuda):
+    """G = 4 runs the LDS-DMA kernel when the cache capacity is a multiple of 32 and the
+    register-staged kernel otherwise; both compute the same arithmetic, so the same prompts in a
+    cache of 256 and of 264 slots give identical bits (and the fp64 bound holds for both)."""
+    lens, NH, NKV = (1, 31, 32, 33, 200, 256), 32, 8
+    B = len(lens)
+    hip = _hip(fake_engine(nh=NH, nkv=NKV, hd=HD))
+    starts = _starts(lens)
+    T = starts[-1]
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(T, NH, HD, generator=g).to(BF)
+    kc = torch.randn(B, NKV, 256, HD, generator=g).to(BF)
+    vc = torch.randn(B, NKV, 256, HD, generator=g).to(BF)
+    kc2 = torch.cat([kc, torch.randn(B, NKV, 8, HD, generator=g).to(BF)], dim=2)
+    vc2 = torch.cat([vc, torch.randn(B, NKV, 8, HD, generator=g).to(BF)], dim=2)
+    ss = torch.tensor(starts, dtype=torch.int32).cuda()
+    qg = q.cuda()
+    dma = hip.attn_prefill_packed(qg, kc.cuda(), vc.cuda(), ss, B, T)
+    reg = hip.attn_prefill_packed(qg, kc2.cuda(), vc2.cuda(), ss, B, T)
+    assert torch.equal(dma, reg)
+    ref = _attn_ref_fp64(q, kc, vc, lens, starts, NH, NKV)
+    assert (dma.double().cpu() - ref).abs().max().item() < 0.02
+    last = torch.tensor(starts[1:]) - 1
+    for k, v in ((kc, vc), (kc2, vc2)):
+        ol = hip.attn_prefill_packed(qg[last].contiguous(), k.cuda(), v.cuda(), ss, B, T, last_only=True)
+        assert torch.equal(ol, dma[last.cuda()])
+
+
 def test_attn_prefill_through_reference_interface(cuda):
     """HipOps.qkv_post(pos=None) + attn_prefill (the reference's ops interface, B prompts of one
     length S) against the oracle's TorchOps on the same qkv."""
