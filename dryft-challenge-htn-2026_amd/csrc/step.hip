@@ -1389,7 +1389,9 @@ __device__ __forceinline__ void run_lm_wide(const Args& a, Shared& sh, int p, bo
 #define DD_SPL_O 0                            // split O as well (80-row steps)
 #endif
 // decode steps split down from this many rows (measured, ms per step, unsplit -> split: B = 16
-// 2.739 -> 2.679, B = 8 2.324 -> 2.301, B = 4 2.167 -> 2.150, B = 1 1.977 -> 1.980)
+// 2.739 -> 2.679, B = 8 2.324 -> 2.301, B = 4 2.167 -> 2.150, B = 1 1.977 -> 1.980); 16-row verify
+// steps take the choice of the decode step of their B sequences, so that the reduction order of
+// their row 0 is the decode step's
 #ifndef DD_SPL_MINM
 #define DD_SPL_MINM 4
 #endif
@@ -1658,9 +1660,17 @@ __host__ __device__ constexpr int att_ovh(int B, int W) {
 #endif
 constexpr int ATT_CB = 4;            // contributors whose partials one combine pass loads
 
-// keys that exist for sequence b this step (its cache below pos plus its W new tokens)
+// Keys the attention of sequence b covers this step: its cache below pos plus its W new tokens,
+// counted as at least ATT_WPAD new tokens (a key past pos + W - 1 is masked for every row, and its
+// cache slot exists: the count stops at cap). The count sets the partition of the key blocks, so a
+// decode step (W = 1) and a verify step of up to ATT_WPAD tokens at the same positions split and
+// combine every (sequence, kv head) pair at the same blocks: row 0 of such a verify step then
+// gives the decode step's bits (speculation stays token-identical to plain decoding).
+#ifndef DD_ATT_WPAD
+#define DD_ATT_WPAD 4
+#endif
 __device__ __forceinline__ int seq_keys(const Args& a, const Shared& sh, int b) {
-  return (int)min<int64_t>(max<int64_t>(sh.pseq[b] + a.W, 0), (int64_t)a.cap);
+  return (int)min<int64_t>(max<int64_t>(sh.pseq[b] + max(a.W, DD_ATT_WPAD), 0), (int64_t)a.cap);
 }
 // every new token of sequence b has a valid cache slot and rope row
 __device__ __forceinline__ bool seq_pos_ok(const Args& a, const Shared& sh, int b) {
@@ -1671,11 +1681,12 @@ __device__ __forceinline__ bool seq_pos_ok(const Args& a, const Shared& sh, int 
 // units[b]: first partition unit of sequence b (sequences with no keys have none);
 // units[B] = total. The partition depends only on this step's positions: computed once per launch.
 //
-// Verify-shaped steps (W > 1) use a pair-aligned partition instead: a segment there costs as much
-// as ~21 blocks (prologue of W G query rows and 2 W new K/V rows, merge of two query tiles,
-// partials), so the unit partition's per-pair overhead units, which a workgroup pays whether or
-// not it holds the pair's blocks, left workgroups with 6 to 43 blocks (ends 14-37 us after the
-// release at B = 16). Here every workgroup holds one segment: pair q gets n_q = ceil(nb_q / X)
+// Verify-shaped steps of the 80-row instantiation (W > 1) use a pair-aligned partition instead: a
+// segment there costs as much as ~21 blocks (prologue of W G query rows and 2 W new K/V rows,
+// merge of two query tiles, partials), so the unit partition's per-pair overhead units, which a
+// workgroup pays whether or not it holds the pair's blocks, left workgroups with 6 to 43 blocks
+// (ends 14-37 us after the release at B = 16). Here every workgroup holds one segment: pair q
+// gets n_q = ceil(nb_q / X)
 // workgroups and an even split of its nb_q blocks, X the smallest share (>= DD_ATT_PAIR_MIN)
 // whose workgroups fit the group.
 #ifndef DD_ATT_PAIR
@@ -1694,10 +1705,13 @@ __device__ __forceinline__ int wave_max_i(int v) {
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
   return v;
 }
+template <int NM>
 __device__ __forceinline__ void attn_partition(const Args& a, Shared& sh, bool flag_errors) {
   const int P = att_groups(a), hpg = a.NKV / P, Gl = (int)gridDim.x / P;
-  const bool pm = DD_ATT_PAIR && a.W > 1 && a.B * hpg <= min(ATT_PAIRS, Gl);
-  const int ovh = pm ? 0 : att_ovh(a.B, a.W);
+  // The 16-row instantiation partitions verify steps (W > 1) exactly as decode steps (unit
+  // partition, the decode weight), so that their row 0 reproduces the decode step.
+  const bool pm = DD_ATT_PAIR && NM > 1 && a.W > 1 && a.B * hpg <= min(ATT_PAIRS, Gl);
+  const int ovh = pm ? 0 : att_ovh(a.B, NM == 1 ? 1 : a.W);
   if (tid() < 64) {                          // wave 0: lane b = sequence b, prefix sum by shuffles
     const int b = tid();
     int cnt = 0;
@@ -2430,7 +2444,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
   {
     // attention phases are p = 2 + 5l: position errors are flagged when one of them runs
     const int l0 = a.phase_begin <= 2 ? 0 : (a.phase_begin - 2 + 4) / 5;
-    attn_partition(a, sh, l0 < a.L && 2 + 5 * l0 < a.phase_end);
+    attn_partition<NM>(a, sh, l0 < a.L && 2 + 5 * l0 < a.phase_end);
   }
   const int nqkv = (a.NH + 2 * a.NKV) * HD;
   // The phases run in their fixed order (embedding; per layer QKV, attention, O, gate/up, down;
@@ -2491,7 +2505,7 @@ __global__ void __launch_bounds__(NTHR, 1) decode_step_kernel(Args a_in) {
     }
     if (in_range(q0 + 4)) {
       SET_PHASE(q0 + 4);
-      if ((NM > 1 || a.M >= DD_SPL_MINM) && res_split_ok(a.I))
+      if ((NM > 1 || a.B >= DD_SPL_MINM) && res_split_ok(a.I))
         run_res_split<M_D, NM>(a, sh, q0 + 4, q0 + 4 > a.phase_begin, epoch_of(q0 + 4),
                            uniform_ptr<const bf16>(lp[F_WD]), a.H, a.I, m_slot(a, layer),
                            2 * layer + 2);

@@ -118,6 +118,37 @@ def small(cuda):
     return ref, eng
 
 
+@pytest.mark.parametrize("B,W", [(1, 4), (2, 4), (3, 2), (4, 4)])
+def test_verify_row0_is_the_decode_step(small, B, W):
+    """A verify step of the 16-row instantiation (B W <= 16, W G <= 16) partitions and reduces
+    like the decode step at the same positions, so its row 0 of every sequence gives the decode
+    step's logits and K/V bit for bit (what makes speculation token-identical to plain decoding).
+    Prompt lengths put positions on, just before and just past 32-key block boundaries."""
+    ref, eng = small
+    g = torch.Generator().manual_seed(100 * B + W)
+    lens = [29, 32, 61, 95][:B]
+    prompts = [torch.randint(0, 1024, (n,), generator=g).tolist() for n in lens]
+    cap = 256
+    sd = eng._new_state(B, cap)
+    eng._prefill(prompts, sd)
+    first = sd.tok.clone()
+    spos = sd.pos.clone()
+    dec = eng.step.run(sd).clone()
+    sv = eng._new_state(B, cap, W=W)
+    eng._prefill(prompts, sv)
+    drafts = torch.randint(0, 1024, (B, W), generator=g)
+    drafts[:, 0] = first.cpu()
+    ver = eng.verify_logits(sv, drafts.cuda(), spos).clone()
+    torch.cuda.synchronize()
+    assert int(sd.err.item()) == 0 and int(sv.err.item()) == 0
+    for b in range(B):
+        assert torch.equal(ver[b * W], dec[b]), b
+        p = int(spos[b])
+        for i in range(eng.L):
+            assert torch.equal(sv.kc[i][b, :, p], sd.kc[i][b, :, p]), (b, i)
+            assert torch.equal(sv.vc[i][b, :, p], sd.vc[i][b, :, p]), (b, i)
+
+
 @pytest.mark.parametrize("W", [2, 4, 5])
 def test_spec_generate_matches_oracle(small, W):
     ref, eng = small
