@@ -419,9 +419,12 @@ def test_speculative_full_size(full):
     speculative stream of each sequence equals plain greedy decode (the one-launch decode step)
     up to its first divergence, if any, and there both tokens are acceptable greedy choices within
     the measured noise: below the torch path's maximum (teacher-forced on the common prefix) by no
-    more than max(2 bf16 ulps, max |decode-step logits - torch logits| of that step). A verify
-    row and a decode step attend the same keys split over workgroups at different points, so
-    their logits differ in the last bits, and a near-tie can resolve either way."""
+    more than max(2 bf16 ulps, max |decode-step logits - torch logits| of that step). These
+    verify steps (B W <= 16) run the 16-row instantiation, which partitions and reduces like the
+    decode step at the same positions, so row 0 of a verify step gives the decode step's bits:
+    with no draft accepted every speculative token is such a row 0 and the streams are identical
+    (asserted). An accepted draft moves the next verify step's positions past tokens whose rows
+    were not row 0, where a block boundary can still split keys differently."""
     from dryft_amd.teacher import decode_trace, first_divergence_check
     cfg, _, eng = full
     V = cfg["vocab_size"]
@@ -448,6 +451,8 @@ def test_speculative_full_size(full):
               f"{stats['accepted_drafts']} accepted drafts, {cnt} tokens, worst gap {worst:.4f}, "
               f"identical to plain decode: {got == plain}; first divergences {divs}")
         assert bad == 0
+        if stats["accepted_drafts"] == 0:
+            assert got == plain
         records.append({"B": len(prompts), "W": W, "tokens": n, "verify_steps": stats["steps"],
                         "accepted_drafts": stats["accepted_drafts"],
                         "identical_to_plain": got == plain, "first_divergences": divs,
