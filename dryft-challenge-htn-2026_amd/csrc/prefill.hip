@@ -581,8 +581,9 @@ DD_API int dd_attn_prefill(const void* q, const void* kc, const void* vc, const 
 // waves per SIMD). configs[4]'s packed prompts, one process alternating builds, us per layer, the
 // same bits throughout: two heads per wave (211 VGPRs, two workgroups per CU) 368; one head per
 // wave with register staging (108 VGPRs) 338; with the LDS-DMA double buffer (116 VGPRs, 32 KB
-// of LDS) 314-322 against 347-354 on the same boxes. Eight waves per workgroup (32 tokens) 370;
-// five or six workgroups per CU spill (349 with DMA; 676 / 805 without). The DMA kernel's last
+// of LDS) 314-322 against 347-354 on the same boxes. Eight waves per workgroup (32 tokens, half
+// the barriers and DMA issues per token) 370, with the DMA double buffer 353 against 320; five or
+// six workgroups per CU spill (349 with DMA; 676 / 805 without). The DMA kernel's last
 // block may reach past a prompt's keys but not past the cache: it needs cap % 32 == 0 (the
 // engine's capacities are multiples of 128), else the register-staged kernel runs.
 #ifndef DD_PF_G4
