@@ -310,21 +310,38 @@ def _time(torch, fn, reps):
 def micro_gemv(torch, eng):
     """the per-op skinny GEMV kernel (dd_gemv, MFMA, in-launch split-K) at the five
     Qwen3-4B projection shapes and M in {1, 4, 8, 16}; bf16 weights N(0, 0.02), x N(0, 1).
-    Bytes per launch = N K 2 + M K 2 + M N 2."""
+    Bytes per launch = N K 2 + M K 2 + M N 2. `us` / `GBps`: the op as generation runs it, inside
+    a captured hipGraph (10 calls per graph, replayed; GPU time per call). `us_eager`: the same
+    op called from Python, which the host's per-call work (two tensor allocations, the ctypes
+    call) bounds at ~12 us whatever the shape."""
     ops = eng.ops.f if hasattr(eng.ops, "f") else eng.ops
     H, I, V = eng.cfg["hidden_size"], eng.cfg["intermediate_size"], eng.cfg["vocab_size"]
     shapes = {"qkv": ((eng.nh + 2 * eng.nkv) * eng.hd, H), "o": (H, eng.nh * eng.hd),
               "gate_up": (2 * I, H), "down": (H, I), "lm_head": (V, H)}
     g = torch.Generator(device="cuda").manual_seed(11)
     out = {}
+    per_graph = 10
     for name, (N, K) in shapes.items():
         w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
         row = {}
         for M in (1, 4, 8, 16):
             x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
-            t = _time(torch, lambda: ops.linear(x, w), 20 if N < 100000 else 5)
-            row[f"M{M}"] = {"us": round(t * 1e6, 2),
-                            "GBps": round((N * K * 2 + M * K * 2 + M * N * 2) / t / 1e9, 1)}
+            te = _time(torch, lambda: ops.linear(x, w), 20 if N < 100000 else 5)
+            ref = ops.linear(x, w)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                ops.linear(x, w)                      # workspace and counters outside capture
+            torch.cuda.current_stream().wait_stream(side)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                ys = [ops.linear(x, w) for _ in range(per_graph)]
+            tg = _time(torch, gr.replay, 5 if N < 100000 else 2) / per_graph
+            assert all(torch.equal(y, ref) for y in ys), f"graph replay differs from eager: {name} M={M}"
+            nb = N * K * 2 + M * K * 2 + M * N * 2
+            row[f"M{M}"] = {"us": round(tg * 1e6, 2), "GBps": round(nb / tg / 1e9, 1),
+                            "us_eager": round(te * 1e6, 2)}
+            del gr, ys
         out[name] = row
         del w
     return out

@@ -209,6 +209,38 @@ gemv_kernel(const bf16* __restrict__ x, const bf16* __restrict__ W, bf16* __rest
   }
 }
 
+// GEMV_OUT without a K split, NR 16-row tiles of W per workgroup: each lane's x load feeds NR
+// MFMAs instead of one (at M = 16 the x operand is as many bytes per k-step as one W tile).
+// Every tile's k order and wave-reduction order are those of gemv_kernel, so the outputs are
+// the same bits. Rows past N are clamped reads whose outputs are not stored.
+template <int U, int NR>
+__global__ void __launch_bounds__(GEMV_THREADS)
+gemv_multi_kernel(const bf16* __restrict__ x, const bf16* __restrict__ W, bf16* __restrict__ y,
+                  int M, int N, int K) {
+  __shared__ float red[(GEMV_WAVES - 1) * NR * 64 * 4];
+  const int n0 = blockIdx.x * 16 * NR;
+  f32x4 acc[NR];
+  int rows[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rows[t] = n0 + 16 * t;
+  }
+  gemv_accumulate<NR, U>(x, M, K, W, rows, N, 0, K, acc);
+  gemv_wave_reduce<NR>(acc, red);
+  if ((threadIdx.x >> 6) != 0) return;
+  const int lane = threadIdx.x & 63;
+  const int m = lane & 15;
+  if (m >= M) return;
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    const int nb = n0 + 16 * t + (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (nb + i < N) y[(size_t)m * N + nb + i] = f2bf(acc[t][i]);
+  }
+}
+
 // Fused gate/up GEMV + SiLU epilogue. Wgu = [gate (I rows); up (I rows)], K columns.
 // out[m][n] = bf16( bf16(silu(bf16 g)) * bf16 u )  -- the rounding points of
 // silu_mul(linear(x, wgu)) in the reference (engine.py:144-146, fused.py:677-682).
@@ -249,13 +281,27 @@ gemv_silu_kernel(const bf16* __restrict__ x, const bf16* __restrict__ Wgu, bf16*
 namespace dd {
 
 // Split-K heuristic for the MI355X (256 CUs): keep one 16-row tile per workgroup and split K
-// until the grid has at least ~2 workgroups per CU, keeping >= 512 k per split.
+// until the grid has at least ~2 workgroups per CU, keeping >= 512 k per split; grids still
+// under 1024 workgroups split further while >= 1024 k per split remain (down, 2560 x 9728: 8
+// splits instead of 4, 15.8 -> 15.3 us at M = 1, 21.8 -> 20.3 at M = 16, graph-timed).
 int pick_splitk(int M, int N, int K) {
   (void)M;
   const int tiles = (N + 15) / 16;
   int sk = 1;
-  while (tiles * sk < 512 && K / (sk * 2) >= 512 && sk < 8) sk *= 2;
+  while (sk < 8 && ((tiles * sk < 512 && K / (sk * 2) >= 512) ||
+                    (tiles * sk < 1024 && K / (sk * 2) >= 1024)))
+    sk *= 2;
   return sk;
+}
+
+// 16-row tiles per workgroup of an unsplit GEMV_OUT launch: at M >= 8 the most (4, 2, 1) that
+// still leave 1024 workgroups. Graph-timed on MI355X, lm_head (151936 x 2560): M = 16 269 -> 223
+// us with four tiles; M = 1 177 -> 200 us (one tile kept there: x is one row, its loads hit the
+// same lines, and four times the workgroups keep more loads in flight).
+int gemv_tiles_per_wg(int M, int N) {
+  const int tiles = (N + 15) / 16;
+  if (M < 8) return 1;
+  return tiles / 4 >= 1024 ? 4 : tiles / 2 >= 1024 ? 2 : 1;
 }
 
 int kps_for(int K, int sk) { return ((K + sk - 1) / sk + 31) / 32 * 32; }
@@ -279,7 +325,14 @@ int launch_gemv(const void* x, const void* W, void* y, void* ws, int* counters, 
   const int kps = kps_for(K, sk);
   const int nsplit = (K + kps - 1) / kps;
   dim3 grid((N + 15) / 16, nsplit);
-  if (h == nullptr)
+  const int nr = h == nullptr && nsplit == 1 ? gemv_tiles_per_wg(M, N) : 1;
+  if (nr == 4)
+    hipLaunchKernelGGL((gemv_multi_kernel<4, 4>), dim3((N + 63) / 64), dim3(GEMV_THREADS), 0,
+                       stream, (const bf16*)x, (const bf16*)W, (bf16*)y, M, N, K);
+  else if (nr == 2)
+    hipLaunchKernelGGL((gemv_multi_kernel<8, 2>), dim3((N + 31) / 32), dim3(GEMV_THREADS), 0, stream,
+                       (const bf16*)x, (const bf16*)W, (bf16*)y, M, N, K);
+  else if (h == nullptr)
     hipLaunchKernelGGL((gemv_kernel<8, GEMV_OUT>), grid, dim3(GEMV_THREADS), 0, stream,
                        (const bf16*)x, (const bf16*)W, (bf16*)y, (float*)ws, counters, M, N, K,
                        kps, nullptr, nullptr, nullptr, 0.f);

@@ -163,10 +163,12 @@ def parse_per_op(trace_dir, pmc_dirs, shapes, reps=10):
     import glob
 
     def dispatches(path, name_filter, counter=None):
+        names = (name_filter,) if isinstance(name_filter, str) else name_filter
         out = []
         with open(path) as f:
             for r in csv.DictReader(f):
-                if name_filter in r["Kernel_Name"] and (counter is None or r["Counter_Name"] == counter):
+                if (any(n in r["Kernel_Name"] for n in names)
+                        and (counter is None or r["Counter_Name"] == counter)):
                     v = float(r["Counter_Value"]) if counter else (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
                     out.append((int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0), v))
         out.sort()
@@ -183,7 +185,9 @@ def parse_per_op(trace_dir, pmc_dirs, shapes, reps=10):
     cal = dispatches(pmc["FETCH_SIZE"], "stream_read_kernel", "FETCH_SIZE")
     scale = (1 << 30) / 1024 / (sum(cal) / len(cal))         # true KiB / counted KiB
     rows = []
-    kinds = [("gemv_kernel", [(n, m) for n in shapes for m in (1, 4, 8, 16)]),
+    # dd_gemv launches gemv_kernel, or gemv_multi_kernel (several W tiles per workgroup) for
+    # unsplit shapes at M >= 8
+    kinds = [(("gemv_kernel", "gemv_multi_kernel"), [(n, m) for n in shapes for m in (1, 4, 8, 16)]),
              ("attn_decode_kernel", [("configs[2]", 16)])]
     for kern, cases in kinds:
         us = dispatches(trace, kern)
@@ -195,7 +199,7 @@ def parse_per_op(trace_dir, pmc_dirs, shapes, reps=10):
             sl = slice(i * (reps + 1) + 1, (i + 1) * (reps + 1))
             mean = lambda v: sum(v[sl]) / len(v[sl])
             t = mean(us)
-            if kern == "gemv_kernel":
+            if "gemv_kernel" in kern:
                 N, K = shapes[name]
                 algo = N * K * 2 + M * K * 2 + M * N * 2
                 label = f"dd_gemv {name} {N}x{K} M={M}"
