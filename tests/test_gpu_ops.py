@@ -185,14 +185,15 @@ def test_gemv_real_shapes(small, weights, name):
         assert (err <= bound + 1e-6).all(), (name, M)
 
 
-@pytest.mark.parametrize("M", [1, 8, 13, 16])
-def test_gemv_multi_tile_exact(small, M):
+@pytest.mark.parametrize("M,N", [(1, 65576), (8, 65576), (13, 65576), (16, 65576), (16, 40008)])
+def test_gemv_multi_tile_exact(small, M, N):
     """N = 65,576 (4,099 tiles of 16 rows, not a multiple of 64 rows) at M >= 8 takes the
-    unsplit kernel with four W tiles per workgroup (M = 1: one tile). Integer x and W in [-3, 3]
-    and K = 512 keep every fp32 partial sum exact in any order, so the one rounding is the bf16
-    store: the fp64 product rounded to bf16 is the exact answer, bit for bit."""
+    unsplit kernel with four W tiles per workgroup (M = 1: one tile); N = 40,008 (2,501 tiles)
+    takes it with two. Integer x and W in [-3, 3] and K = 512 keep every fp32 partial sum exact
+    in any order, so the one rounding is the bf16 store: the fp64 product rounded to bf16 is the
+    exact answer, bit for bit."""
     _, hip, _ = small
-    N, K = 65576, 512
+    K = 512
     g = torch.Generator().manual_seed(40 + M)
     x = torch.randint(-3, 4, (M, K), generator=g).to(BF)
     w = torch.randint(-3, 4, (N, K), generator=g).to(BF)
